@@ -1,0 +1,162 @@
+/*
+ * uocr_moe -- the DeepSeek-V2 routed-expert MoE block of unlimited-ocr-max on
+ * AMD Instinct MI355X (gfx950), behind a plain C ABI.
+ *
+ * Every entry point takes device pointers (HIP memory), the shapes of each
+ * tensor as the reference's ops see them, a HIP stream (NULL = the null
+ * stream) and an optional error buffer.  The work is enqueued on the stream
+ * and the call returns without waiting.  Return value: 0 on success, nonzero
+ * on a refused call, with the reference's message text ("<op>: <reason>")
+ * copied into err (NUL-terminated, truncated to errlen).  Shape checks run on
+ * the host before anything is enqueued; device-side the ops never fail:
+ * out-of-range expert ids are clamped to [0, E).
+ *
+ * Tensors are row-major and packed.  bf16 tensors are passed as uint16_t bit
+ * patterns.  The library keeps no pointer past the call.  Scratch memory for
+ * the grouping tables and the layer intermediates comes from the `workspace`
+ * argument when one is given (size: uocr_moe_workspace_bytes), else from a
+ * buffer the library keeps per device and stream (grown on demand).
+ */
+#ifndef UOCR_MOE_H
+#define UOCR_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UOCR_MOE_ABI_VERSION 1
+
+int uocr_moe_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * The reference's custom ops (the MAX @register ops of the Mojo files in
+ * unlimited_ocr_max/kernels/), one entry point each.
+ * ------------------------------------------------------------------------- */
+
+/* moe_int8_qmv -- replaces MoeInt8Qmv.execute
+ * (unlimited_ocr_max/kernels/moe_int8.mojo:181-258; staged by
+ * StackedExperts._qmv, unlimited_ocr_max/decoder.py:355-366).
+ *   result fp32 [k, N], x fp32 [k, K], expert_ids int32 [k],
+ *   w int8 [E, N, K], scales fp32 [E, N, K/G]
+ *   result[s,n] = sum_g scales[e,n,g] * sum_{kk in g} f32(w[e,n,kk]) * x[s,kk],
+ *   e = clamp(expert_ids[s]); bitwise the reference's operation order
+ *   (a per-group fma chain in kk order, then fma(scale, gsum, acc) per group). */
+int uocr_moe_int8_qmv(float* result, int64_t result_k, int64_t result_n,
+                      const float* x, int64_t x_k, int64_t x_kdim,
+                      const int32_t* expert_ids, int64_t ids_k,
+                      const int8_t* w, int64_t w_e, int64_t w_n, int64_t w_kdim,
+                      const float* scales, int64_t s_e, int64_t s_n, int64_t s_groups,
+                      void* stream, char* err, size_t errlen);
+
+/* moe_bf16_qmv -- replaces MoeBf16Qmv.execute
+ * (unlimited_ocr_max/kernels/moe_bf16.mojo:264-345).
+ *   result fp32 [k, N], x fp32 [k, K], expert_ids int32 [k], w bf16 [E, N, K]
+ *   result[s,n] = sum_kk f32(w[e,n,kk]) * x[s,kk], fp32 accumulation in
+ *   128-element chunks (fma chain per chunk, chunk sums added in order). */
+int uocr_moe_bf16_qmv(float* result, int64_t result_k, int64_t result_n,
+                      const float* x, int64_t x_k, int64_t x_kdim,
+                      const int32_t* expert_ids, int64_t ids_k,
+                      const uint16_t* w, int64_t w_e, int64_t w_n, int64_t w_kdim,
+                      void* stream, char* err, size_t errlen);
+
+/* int8_dequant_expert -- replaces Int8DequantExpert.execute
+ * (unlimited_ocr_max/kernels/moe_int8.mojo:261-342; staged by
+ * StackedExperts._dequant, unlimited_ocr_max/decoder.py:325-330).
+ *   result [N, K] bf16 (result_f32 = 0) or fp32 (result_f32 = 1),
+ *   w int8 [E, N, K], scales fp32 [E, N, K/G], expert_idx int32 [1] (device)
+ *   result[n,kk] = round(f32(w[e,n,kk]) * scales[e,n,kk/G]), e = clamp(idx),
+ *   bf16 by round-to-nearest-even. */
+int uocr_int8_dequant_expert(void* result, int64_t result_n, int64_t result_kdim, int result_f32,
+                             const int8_t* w, int64_t w_e, int64_t w_n, int64_t w_kdim,
+                             const float* scales, int64_t s_e, int64_t s_n, int64_t s_groups,
+                             const int32_t* expert_idx, int64_t idx_len,
+                             void* stream, char* err, size_t errlen);
+
+/* dense_bf16_qmv -- replaces DenseBf16Qmv.execute[tile]
+ * (unlimited_ocr_max/kernels/dense_bf16.mojo:119-158; staged by
+ * dense_bf16_qmv, unlimited_ocr_max/decoder.py:166-184).
+ *   result fp32 [M, N], x fp32 [M, K], w bf16 K-blocked [K/16, N, 16]
+ *   result[m,n] = sum_kk f32(W[n,kk]) * x[m,kk], W[n,kk] = w[kk/16, n, kk%16].
+ *   `tile` (>= 1) is the reference's rows-per-read parameter; a row's bits
+ *   do not depend on it. */
+int uocr_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n,
+                        const float* x, int64_t x_m, int64_t x_kdim,
+                        const uint16_t* w, int64_t w_blocks, int64_t w_n, int64_t w_kblock,
+                        int64_t tile, void* stream, char* err, size_t errlen);
+
+/* ---------------------------------------------------------------------------
+ * The MoE block.
+ * ------------------------------------------------------------------------- */
+
+/* One MoE layer's weights (unlimited_ocr_max/decoder.py:517-554, declared
+ * names in StackedExperts.__init__, decoder.py:297-313):
+ *   router             fp32 [E, H]                 gate.gate_score.weight
+ *   gate_proj/up_proj  [E, F, H], down_proj [E, H, F]   experts.*
+ *                      int8 (int8 = 1) or bf16 bits (int8 = 0)
+ *   *_scales           fp32 [E, F, H/G], [E, F, H/G], [E, H, F/G] (int8 only)
+ *   shared_*           bf16 bits, K-blocked: gate/up [H/16, Fs, 16],
+ *                      down [Fs/16, H, 16]          shared_experts.*
+ * E <= 64.  renormalize = 0 is the reference's gate (model_config.py:149-150);
+ * 1 divides the top-k weights by their sum. */
+typedef struct uocr_moe_layer {
+  int64_t num_experts; /* E */
+  int64_t hidden;      /* H */
+  int64_t ffn;         /* F, moe_intermediate_size */
+  int64_t shared_ffn;  /* Fs = n_shared_experts * F */
+  int64_t top_k;
+  int64_t group;       /* int8 group size along K (128) */
+  int32_t int8;
+  int32_t renormalize;
+  const float* router;
+  const void* gate_proj;
+  const void* up_proj;
+  const void* down_proj;
+  const float* gate_proj_scales;
+  const float* up_proj_scales;
+  const float* down_proj_scales;
+  const uint16_t* shared_gate;
+  const uint16_t* shared_up;
+  const uint16_t* shared_down;
+} uocr_moe_layer;
+
+/* Bytes of workspace the layer entries need for `rows` tokens
+ * (prefill = 0: uocr_moe_decode_rows, 1: uocr_moe_forward). */
+size_t uocr_moe_workspace_bytes(const uocr_moe_layer* layer, int64_t rows, int prefill);
+
+/* MoEGate.__call__ -- replaces the gate of unlimited_ocr_max/decoder.py:509-514
+ * (router matmul + ops.softmax + ops.top_k).
+ *   indices int64 [T, k], weights fp32 [T, k] in score order, ties to the
+ *   lower id; x fp32 [T, H], router fp32 [E, H], E <= 64. */
+int uocr_moe_gate(int64_t* indices, float* weights, const float* x, int64_t seq, int64_t hidden,
+                  const float* router, int64_t num_experts, int64_t top_k, int renormalize,
+                  void* workspace, size_t workspace_bytes, void* stream, char* err, size_t errlen);
+
+/* MoE.decode_rows -- replaces unlimited_ocr_max/decoder.py:641-655 (gate,
+ * _routed_qmv through moe_int8_qmv / moe_bf16_qmv, SwiGLU, _mix, shared
+ * experts through dense_bf16_qmv).  x fp32 [B, H] -> out fp32 [B, H], B <= 64.
+ * Bitwise the CPU oracle's or_moe_decode_exact.  expert_ids / expert_weights
+ * (device, [B, k], may be NULL) receive the routing. */
+int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidden,
+                         const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
+                         void* workspace, size_t workspace_bytes, void* stream, char* err, size_t errlen);
+
+/* MoE.__call__ (prefill) -- replaces unlimited_ocr_max/decoder.py:657-667
+ * (the dense 64-expert chain of the int8 path, _routed_native of the bf16
+ * path).  x fp32 [T, H] -> out fp32 [T, H].  The top-k experts of every token
+ * run as a grouped GEMM on the bf16 matrix cores: int8 weights dequantised to
+ * bf16_rne(f32(q)*scale) (the reference's prefill values), activations
+ * rounded to bf16, fp32 accumulation.  H, F, Fs multiples of 128. */
+int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden,
+                     const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
+                     void* workspace, size_t workspace_bytes, void* stream, char* err, size_t errlen);
+
+/* Frees the library's own workspaces (those used when workspace == NULL). */
+void uocr_moe_release(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

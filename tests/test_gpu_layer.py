@@ -1,0 +1,172 @@
+"""GPU parity of the MoE block (gate, decode layer, prefill layer) against the CPU oracle.
+
+* gate: ids and weights bitwise the oracle's ``or_moe_gate`` (which is pinned to
+  the float64 softmax + stable argsort); ties go to the lower id.
+* decode (``MoE.decode_rows``): bitwise the oracle's ``or_moe_decode_exact``, and
+  within the reference's module bars of the float64 layer (cosine >= 0.99999,
+  rel <= 1e-4; tests/test_decoder_int8.py:740-807); rows bitwise their one-row
+  values.
+* prefill (``MoE.__call__``): expert ids bitwise the oracle gate; output within
+  max relative error 1e-2 of the float64 layer on the reference's prefill
+  weights, ``bf16_rne(f32(q) * scale)`` (the int8 path's int8_dequant_expert values;
+  decoder.py:568-584) -- the north-star tolerance for the bf16-MFMA layer.
+  Shapes: the served layer (64 experts, 1280/896, 2 shared) at T = 64 and 512,
+  with Zipf-skewed and adversarial (all tokens on experts 0-5) routing.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu import bits_equal, differ, moe_for, n, t
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def small(oracle):
+    return {i8: oracle.make_layer(19, E=8, H=256, F=128, int8=i8, std=0.05, router_std=0.1) for i8 in (True, False)}
+
+
+@pytest.fixture(scope="module")
+def full_int8(oracle):
+    return oracle.make_layer(1, int8=True)
+
+
+@pytest.fixture(scope="module")
+def full_bf16(oracle):
+    return oracle.make_layer(2, int8=False)
+
+
+# ----------------------------------------------------------------------------- gate
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 300, 4096])
+def test_gate_bitwise(oracle, T) -> None:
+    from uocr_moe import gate
+
+    rng = np.random.default_rng(T)
+    x = oracle.rmsnorm_rows(rng, T, 1280)
+    router = oracle.bf16_values(oracle.bf16_bits(rng.standard_normal((64, 1280), dtype=np.float32) * np.float32(0.02)))
+    idx, wts = gate(t(x), t(router), 6)
+    ids_o, wts_o = oracle.moe_gate(x, router, 6)
+    assert np.array_equal(n(idx), ids_o.astype(np.int64))
+    assert bits_equal(n(wts), wts_o)
+
+
+def test_gate_ties_and_renorm(oracle) -> None:
+    from uocr_moe import gate
+
+    x = np.ones((2, 64), np.float32)
+    router = np.zeros((8, 64), np.float32)
+    router[[1, 5, 6], :] = 0.01
+    idx, wts = gate(t(x), t(router), 6)
+    assert n(idx)[0].tolist() == [1, 5, 6, 0, 2, 3]
+    idx, wts = gate(t(x), t(router), 6, renormalize=True)
+    _, w_o = oracle.moe_gate(x, router, 6, renorm=True)
+    assert bits_equal(n(wts), w_o)
+
+
+# ----------------------------------------------------------------------------- decode
+
+
+@pytest.mark.parametrize("int8", [True, False], ids=["int8", "bf16"])
+def test_decode_small_layer_bitwise(oracle, small, int8) -> None:
+    layer = small[int8]
+    moe = moe_for(layer)
+    x = np.random.default_rng(23).standard_normal((8, 256)).astype(np.float32)
+    out, ids, wts = moe.decode_rows(t(x), routing=True)
+    want, ids_o, wts_o = oracle.moe_decode_exact(x, layer)
+    print(f"[uocr] decode small {'int8' if int8 else 'bf16'}: {differ(n(out), want)} differ")
+    assert np.array_equal(n(ids), ids_o) and bits_equal(n(wts), wts_o)
+    assert bits_equal(n(out), want)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_decode_full_int8_bitwise(oracle, full_int8, B) -> None:
+    moe = moe_for(full_int8)
+    x = oracle.rmsnorm_rows(np.random.default_rng(100 + B), B, 1280)
+    out, ids, wts = moe.decode_rows(t(x), routing=True)
+    got = n(out)
+    want, ids_o, wts_o = oracle.moe_decode_exact(x, full_int8)
+    print(f"[uocr] decode int8 B={B}: {differ(got, want)} of {got.size} differ")
+    assert np.array_equal(n(ids), ids_o)
+    assert bits_equal(got, want)
+    exact = oracle.moe_layer_f64(x, full_int8, ids_o, wts_o)
+    assert min(oracle.cosine(got[i], exact[i]) for i in range(B)) >= 0.99999
+    assert oracle.rel_err(got, exact) <= 1e-4
+    if B > 1:
+        single = np.concatenate([n(moe.decode_rows(t(x[i : i + 1]))) for i in range(B)])
+        assert bits_equal(got, single)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_decode_full_bf16_bitwise(oracle, full_bf16, B) -> None:
+    moe = moe_for(full_bf16)
+    x = oracle.rmsnorm_rows(np.random.default_rng(200 + B), B, 1280)
+    got = n(moe.decode_rows(t(x)))
+    want, ids_o, wts_o = oracle.moe_decode_exact(x, full_bf16)
+    assert bits_equal(got, want)
+    exact = oracle.moe_layer_f64(x, full_bf16, ids_o, wts_o)
+    assert oracle.rel_err(got, exact) <= 1e-4
+
+
+def test_decode_batch_of_64_and_workspace(oracle, small) -> None:
+    layer = small[True]
+    moe = moe_for(layer)
+    x = np.random.default_rng(5).standard_normal((64, 256)).astype(np.float32)
+    ws = moe.workspace(64, prefill=False)
+    got = n(moe.decode_rows(t(x), workspace=ws))
+    assert bits_equal(got, oracle.moe_decode_exact(x, layer)[0])
+    with pytest.raises(Exception, match="rows must be in"):
+        moe.decode_rows(t(np.zeros((65, 256), np.float32)))
+
+
+# ----------------------------------------------------------------------------- prefill
+
+
+@pytest.mark.parametrize(("which", "T"), [("int8", 64), ("int8", 512), ("bf16", 512)])
+def test_prefill_matches_float64(oracle, full_int8, full_bf16, which, T) -> None:
+    layer = full_int8 if which == "int8" else full_bf16
+    moe = moe_for(layer)
+    x = oracle.rmsnorm_rows(np.random.default_rng(300 + T), T, 1280)
+    out, ids, wts = moe(t(x), routing=True)
+    ids_o, wts_o = oracle.moe_gate(x, layer.router, 6)
+    assert np.array_equal(n(ids), ids_o) and bits_equal(n(wts), wts_o)
+    got = n(out)
+    ref = oracle.moe_layer_f64(x, layer, ids_o, wts_o, bf16_dequant=True)
+    rel = oracle.rel_err(got, ref)
+    print(f"[uocr] prefill {which} T={T}: rel {rel:.3e}, min cos {min(oracle.cosine(got[i], ref[i]) for i in range(T)):.6f}")
+    assert rel <= 1e-2
+    assert np.all(np.isfinite(got))
+
+
+def test_prefill_adversarial_routing(oracle, full_int8) -> None:
+    """Router logits +10 on experts 0-5 for every token: six groups of all T tokens."""
+    import dataclasses
+
+    x = oracle.rmsnorm_rows(np.random.default_rng(7), 512, 1280)
+    x[:, 0] = 10.0
+    router = full_int8.router.copy()
+    router[:, 0] = 0.0
+    router[:6, 0] = 1.0
+    adv = dataclasses.replace(full_int8, router=np.ascontiguousarray(router))
+    moe = moe_for(adv)
+    out, ids, wts = moe(t(x), routing=True)
+    ids_o, wts_o = oracle.moe_gate(x, adv.router, 6)
+    assert np.array_equal(n(ids), ids_o)
+    assert np.all(np.sort(ids_o, axis=1) == np.arange(6)[None, :])
+    got = n(out)
+    ref = oracle.moe_layer_f64(x, adv, ids_o, wts_o, bf16_dequant=True)
+    assert oracle.rel_err(got, ref) <= 1e-2
+
+
+def test_prefill_rows_do_not_depend_on_the_batch(oracle, full_int8) -> None:
+    """A token's prefill output does not depend on which tokens share its call (row-independent tiles)."""
+    moe = moe_for(full_int8)
+    x = oracle.rmsnorm_rows(np.random.default_rng(9), 96, 1280)
+    whole = n(moe(t(x)))
+    part = n(moe(t(x[:40])))
+    assert bits_equal(whole[:40], part)

@@ -1,0 +1,103 @@
+"""The HIP library loads, exports every entry point ``include/uocr_moe.h`` declares, and
+refuses mis-shaped calls with the reference's messages before touching the GPU.
+
+No compute is launched here (no GPU needed): each refused call fails in the
+host-side shape checks, which run before anything is enqueued
+(unlimited_ocr_max/kernels/moe_int8.mojo:194-210, moe_bf16.mojo:276-285,
+dense_bf16.mojo:130-144, moe_int8.mojo:280-296).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "uocr_moe.h"
+
+
+def _declared() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(uocr_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points() -> None:
+    names = _declared()
+    for want in ("uocr_moe_int8_qmv", "uocr_moe_bf16_qmv", "uocr_int8_dequant_expert", "uocr_dense_bf16_qmv",
+                 "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    from uocr_moe import _lib
+
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert lib.uocr_moe_abi_version() == 1
+
+
+def _err(name: str, *args) -> str:
+    from uocr_moe import _lib
+
+    with pytest.raises(_lib.UocrError) as info:
+        _lib.call(name, *args)
+    return str(info.value)
+
+
+@pytest.mark.parametrize(
+    ("dims", "message"),
+    [
+        ((2, 4, 3, 32, 2, 3, 4, 32, 3, 4, 4), "moe_int8_qmv: x and output disagree on k"),
+        ((2, 4, 2, 32, 3, 3, 4, 32, 3, 4, 4), "moe_int8_qmv: expert_ids and output disagree on k"),
+        ((2, 4, 2, 32, 2, 3, 5, 32, 3, 5, 4), "moe_int8_qmv: w and output disagree on N"),
+        ((2, 4, 2, 24, 2, 3, 4, 32, 3, 4, 4), "moe_int8_qmv: w and x disagree on K"),
+        ((2, 4, 2, 32, 2, 0, 4, 32, 0, 4, 4), "moe_int8_qmv: the expert stack is empty"),
+        ((2, 4, 2, 32, 2, 3, 4, 32, 2, 4, 4), "moe_int8_qmv: scales and w disagree on E"),
+        ((2, 4, 2, 32, 2, 3, 4, 32, 3, 5, 4), "moe_int8_qmv: scales and w disagree on N"),
+        ((2, 4, 2, 32, 2, 3, 4, 32, 3, 4, 5), "moe_int8_qmv: K must be a multiple of the group count"),
+        ((2, 4, 2, 32, 2, 3, 4, 32, 3, 4, 0), "moe_int8_qmv: K must be a multiple of the group count"),
+    ],
+)
+def test_int8_qmv_refusals(dims, message: str) -> None:
+    rk, rn, xk, xK, ik, we, wn, wK, se, sn, sg = dims
+    got = _err("uocr_moe_int8_qmv", None, rk, rn, None, xk, xK, None, ik, None, we, wn, wK, None, se, sn, sg, None)
+    assert got == message
+
+
+def test_bf16_qmv_refusals() -> None:
+    assert _err("uocr_moe_bf16_qmv", None, 2, 4, None, 2, 24, None, 2, None, 3, 4, 32, None) == \
+        "moe_bf16_qmv: w and x disagree on K"
+    assert _err("uocr_moe_bf16_qmv", None, 2, 4, None, 2, 32, None, 2, None, 0, 4, 32, None) == \
+        "moe_bf16_qmv: the expert stack is empty"
+
+
+def test_dequant_refusals() -> None:
+    assert _err("uocr_int8_dequant_expert", None, 4, 32, 0, None, 3, 4, 32, None, 3, 4, 5, None, 1, None) == \
+        "int8_dequant_expert: K must be a multiple of the group count"
+    assert _err("uocr_int8_dequant_expert", None, 4, 32, 0, None, 3, 4, 32, None, 3, 4, 4, None, 2, None) == \
+        "int8_dequant_expert: `expert_idx` must be a single int32"
+
+
+def test_dense_refusals() -> None:
+    assert _err("uocr_dense_bf16_qmv", None, 2, 4, None, 2, 24, None, 2, 4, 16, 1, None) == \
+        "dense_bf16_qmv: w and x disagree on K"
+    assert _err("uocr_dense_bf16_qmv", None, 2, 4, None, 2, 32, None, 4, 4, 8, 1, None) == \
+        "dense_bf16_qmv: w is not K-blocked by KBLOCK"
+    assert _err("uocr_dense_bf16_qmv", None, 2, 4, None, 2, 32, None, 2, 4, 16, 0, None) == \
+        "dense_bf16_qmv: tile must be >= 1"
+
+
+def test_layer_refusals() -> None:
+    from uocr_moe import _lib
+
+    layer = _lib.Layer(65, 1280, 896, 1792, 6, 128, 1, 0)
+    msg = _err("uocr_moe_decode_rows", None, None, 1, 1280, ctypes.byref(layer), None, None, None, 0, None)
+    assert msg == "uocr_moe_decode_rows: num_experts must be in [1, 64]"
+    layer = _lib.Layer(64, 1280, 896, 1792, 6, 128, 1, 0)
+    msg = _err("uocr_moe_forward", None, None, 1, 1024, ctypes.byref(layer), None, None, None, 0, None)
+    assert msg == "uocr_moe_forward: x and the layer disagree on hidden"

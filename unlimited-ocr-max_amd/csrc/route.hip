@@ -1,0 +1,240 @@
+// Routing: router logits, softmax + top-k, grouping of routed rows by expert,
+// and the routing-weighted combine.
+//
+// Arithmetic (restated by the CPU oracle):
+//   logit[t,e] = 64 lane fma chains over k = lane, lane+64, ... of x[t,k]*Wr[e,k],
+//                then a halving tree over the lanes (v[l] += v[l+off], off 32..1);
+//   p = uexp(l - max) / S, S the same halving tree over the 64 expert slots;
+//   top-k in score order, ties to the lower id (unlimited_ocr_max/decoder.py:509-514,
+//   no renormalisation unless asked: model_config.py:149-150);
+//   combine: fma chain over the k slots from 0, then + shared
+//   (decoder.py:599-604,655).
+#include "uocr_device.h"
+#include "uocr_kernels.h"
+
+namespace uocr {
+
+namespace {
+
+// ---------------------------------------------------------------- logits
+
+template <int TT, int EE>
+__global__ void __launch_bounds__(256) k_logits(float* __restrict__ logits, const float* __restrict__ x,
+                                                int64_t ldx, const float* __restrict__ router, int T, int E,
+                                                int H) {
+  const int w = (int)(threadIdx.x >> 6);
+  const int lane = lane_id();
+  const int e0 = ((int)blockIdx.x * 4 + w) * EE;
+  const int t0 = (int)blockIdx.y * TT;
+  if (e0 >= E) return;
+  const float* xr[TT];
+  const float* wr[EE];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) xr[t] = x + (int64_t)min(t0 + t, T - 1) * ldx;
+#pragma unroll
+  for (int e = 0; e < EE; ++e) wr[e] = router + (int64_t)min(e0 + e, E - 1) * H;
+  float p[TT][EE];
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int e = 0; e < EE; ++e) p[t][e] = 0.0f;
+  for (int k = lane; k < H; k += kWave) {
+    float xv[TT], wv[EE];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) xv[t] = xr[t][k];
+#pragma unroll
+    for (int e = 0; e < EE; ++e) wv[e] = wr[e][k];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int e = 0; e < EE; ++e) p[t][e] = __builtin_fmaf(xv[t], wv[e], p[t][e]);
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int e = 0; e < EE; ++e) {
+      const float v = wave_tree_sum(p[t][e]);
+      if (lane == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = v;
+    }
+}
+
+// ---------------------------------------------------------------- softmax + top-k
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One wave: softmax over the E <= 64 logits of one token and its top-k.
+// Lane 0 writes the results; returns nothing else.
+__device__ void token_topk(const float* __restrict__ lrow, int E, int topk, int renorm, int32_t* ids32,
+                           int64_t* ids64, float* wts, int32_t* lds_ids) {
+  const int l = lane_id();
+  const float v = l < E ? lrow[l] : -__builtin_huge_valf();
+  const float m = wave_max(v);
+  const float ex = l < E ? uexp(v - m) : 0.0f;
+  const float S = __shfl(wave_tree_sum(ex), 0, kWave);
+  const float p = l < E ? ex / S : 0.0f;
+  uint64_t key = l < E ? (((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(kWave - l)) : 0ull;
+  float d = 0.0f;  // the renormaliser, summed in selection order
+  for (int j = 0; j < topk; ++j) {
+    const uint64_t best = wave_max_u64(key);
+    const int sel = kWave - (int)(best & 0xFFFFFFFFu);
+    const float ws = __shfl(p, sel, kWave);
+    d = d + ws;
+    if (l == sel) key = 0ull;
+    if (l == 0) {
+      if (ids32) ids32[j] = sel;
+      if (ids64) ids64[j] = sel;
+      if (wts) wts[j] = ws;
+      if (lds_ids) lds_ids[j] = sel;
+    }
+  }
+  if (renorm && wts && l == 0)
+    for (int j = 0; j < topk; ++j) wts[j] = wts[j] / d;
+}
+
+__global__ void __launch_bounds__(256) k_softmax_topk(const float* __restrict__ logits, int T, int E, int topk,
+                                                      int renorm, int32_t* ids32, int64_t* ids64, float* wts) {
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= T) return;
+  const int64_t o = (int64_t)t * topk;
+  token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 ? ids32 + o : nullptr, ids64 ? ids64 + o : nullptr,
+             wts ? wts + o : nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------- grouping
+
+constexpr int kMaxGroupExperts = 1024;
+
+// Groups R rows by clamped expert id; `idof(r)` returns row r's raw id.
+// Counts are exact; within a group the row order is whatever the LDS atomics
+// give, which no output depends on (each row is computed on its own).
+template <typename IdOf>
+__device__ void group_rows(IdOf idof, int R, int E, int bm, const GroupTables& g, int* cnt, int* cursor) {
+  const int tid = (int)threadIdx.x;
+  const int nt = (int)blockDim.x;
+  for (int e = tid; e < E; e += nt) cnt[e] = 0;
+  __syncthreads();
+  for (int r = tid; r < R; r += nt) atomicAdd(&cnt[clamp_expert(idof(r), E)], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int off = 0, ng = 0, tiles = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = cnt[e];
+      cursor[e] = off;
+      if (c > 0) {
+        stg(g.group_expert + ng, e);
+        stg(g.group_start + ng, off);
+        if (g.tile_start) stg(g.tile_start + ng, tiles);
+        tiles += (c + bm - 1) / bm;
+        ++ng;
+      }
+      off += c;
+    }
+    stg(g.group_start + ng, off);
+    if (g.tile_start) stg(g.tile_start + ng, tiles);
+    stg(g.n_groups, ng);
+  }
+  __syncthreads();
+  for (int r = tid; r < R; r += nt) {
+    const int pos = atomicAdd(&cursor[clamp_expert(idof(r), E)], 1);
+    stg(g.group_rows + pos, r);
+    if (g.inv) stg(g.inv + r, pos);
+  }
+}
+
+__global__ void __launch_bounds__(1024) k_group(const int32_t* __restrict__ ids, int R, int E, int bm, GroupTables g) {
+  __shared__ int cnt[kMaxGroupExperts];
+  __shared__ int cursor[kMaxGroupExperts];
+  group_rows([&](int r) { return ids[r]; }, R, E, bm, g, cnt, cursor);
+}
+
+constexpr int kSmallTokens = 64;
+
+__global__ void __launch_bounds__(1024) k_route_small(const float* __restrict__ logits, int T, int E, int topk,
+                                                      int renorm, int32_t* ids32, float* wts, GroupTables g) {
+  __shared__ int cnt[kMaxGroupExperts];
+  __shared__ int cursor[kMaxGroupExperts];
+  __shared__ int ids_lds[kSmallTokens * 64];
+  const int nw = (int)(blockDim.x >> 6);
+  for (int t = (int)(threadIdx.x >> 6); t < T; t += nw) {
+    const int64_t o = (int64_t)t * topk;
+    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + o);
+  }
+  __syncthreads();
+  group_rows([&](int r) { return ids_lds[r]; }, T * topk, E, 1, g, cnt, cursor);
+}
+
+// ---------------------------------------------------------------- combine
+
+__global__ void __launch_bounds__(256) k_combine(float* __restrict__ out, const float* __restrict__ y, int64_t ldy,
+                                                 const float* __restrict__ wts, const int32_t* __restrict__ inv,
+                                                 const float* __restrict__ shared, int T, int H, int topk) {
+  const int t = (int)blockIdx.y;
+  const int n = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (n >= H) return;
+  float acc = 0.0f;
+  for (int j = 0; j < topk; ++j) {
+    const int i = t * topk + j;
+    const int row = inv ? inv[i] : i;
+    acc = __builtin_fmaf(wts[i], y[(int64_t)row * ldy + n], acc);
+  }
+  out[(int64_t)t * H + n] = shared ? acc + shared[(int64_t)t * H + n] : acc;
+}
+
+}  // namespace
+
+hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E, int H,
+                         hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (T <= 8) {
+    // decode: one wave per expert, every token of the step against it
+    const dim3 grid((E + 3) / 4, 1);
+    hipLaunchKernelGGL((k_logits<8, 1>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
+  } else {
+    const dim3 grid((E + 15) / 16, (T + 15) / 16);
+    hipLaunchKernelGGL((k_logits<16, 4>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_softmax_topk(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
+                               int64_t* ids64, float* wts, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_softmax_topk, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, topk, renorm, ids32, ids64,
+                     wts);
+  return hipGetLastError();
+}
+
+hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s) {
+  if (E > kMaxGroupExperts) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, s, ids, R, E, bm, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
+                              const GroupTables& g, hipStream_t s) {
+  if (T > kSmallTokens || E > 64 || topk > 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_route_small, dim3(1), dim3(1024), 0, s, logits, T, E, topk, renorm, ids32, wts, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* wts, const int32_t* inv,
+                          const float* shared, int T, int H, int topk, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, T), dim3(256), 0, s, out, y, ldy, wts, inv, shared, T, H, topk);
+  return hipGetLastError();
+}
+
+}  // namespace uocr

@@ -1,0 +1,143 @@
+// Device-side helpers shared by the MoE kernels (gfx950, wave64).
+//
+// Every rounding here is part of the decode path's arithmetic contract: the
+// CPU oracle evaluates the same steps in the same order, so results agree bit
+// for bit.  The build passes -ffp-contract=off, so the only fused
+// multiply-adds are the explicit __builtin_fmaf calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "uocr_kernels.h"
+
+namespace uocr {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+#define UOCR_GLOBAL __attribute__((address_space(1)))
+#define UOCR_CONST __attribute__((address_space(4)))
+
+// A 16-byte global load that bypasses cache retention: the expert weights
+// are read once per call, so they should not evict activations and tables.
+// (Pointers reach the kernels inside argument structs, where the compiler
+// sees generic pointers; the casts state the global address space.)
+__device__ __forceinline__ int4 load_nt16(const void* p) {
+  const i32x4 v = __builtin_nontemporal_load((const UOCR_GLOBAL i32x4*)p);
+  return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 load_nt16u(const void* p) {
+  const i32x4 v = __builtin_nontemporal_load((const UOCR_GLOBAL i32x4*)p);
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
+__device__ __forceinline__ float4 ldg_f4(const void* p) {
+  const f32x4 v = *(const UOCR_GLOBAL f32x4*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ldg_u4(const void* p) {
+  const i32x4 v = *(const UOCR_GLOBAL i32x4*)p;
+  return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
+// Plain global load of a scalar.
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+  return *(const UOCR_GLOBAL T*)p;
+}
+
+// A load of memory no thread writes during the kernel, through the constant
+// address space: at a wave-uniform address it becomes a scalar load.
+template <typename T>
+__device__ __forceinline__ T ldc(const T* p) {
+  return *(const UOCR_CONST T*)p;
+}
+
+template <typename T>
+__device__ __forceinline__ void stg(T* p, T v) {
+  *(UOCR_GLOBAL T*)p = v;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// The low and high bf16 of a packed pair, widened exactly.
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xFFFF0000u); }
+
+// fp32 -> bf16 bits, round-to-nearest-even, NaN -> 0x7FC0.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  if (f != f) return 0x7FC0;
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Two fp32 -> packed bf16 pair (lo in the low half), round-to-nearest-even
+// (v_cvt_pk_bf16_f32).  Same bits as f32_to_bf16_rne for every non-NaN input.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v.x = (__bf16)lo;
+  v.y = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float pow2i(int n) { return __uint_as_float((uint32_t)(n + 127) << 23); }
+
+// exp(x): Cody-Waite reduction by ln 2 (16-bit head + tail), the degree-7
+// Taylor polynomial of e^r on |r| <= ln2/2 in Horner form, two exact
+// power-of-two scalings.  Within 2 ulp of exp over the fp32 range.
+__device__ __forceinline__ float uexp(float x) {
+  if (x != x) return x;
+  if (x > 88.72283f) return __builtin_huge_valf();
+  if (x < -103.972f) return 0.0f;
+  const float t = x * 1.44269502f;
+  const float n = __builtin_rintf(t);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860677e-06f, r);
+  float p = 1.98412701e-04f;
+  p = __builtin_fmaf(p, r, 1.38888892e-03f);
+  p = __builtin_fmaf(p, r, 8.33333377e-03f);
+  p = __builtin_fmaf(p, r, 4.16666679e-02f);
+  p = __builtin_fmaf(p, r, 1.66666672e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int n1 = ni / 2;
+  const int n2 = ni - n1;
+  return (p * pow2i(n1)) * pow2i(n2);
+}
+
+// silu(g) = g / (1 + exp(-g)), each step rounded to fp32 (IEEE division).
+__device__ __forceinline__ float silu(float g) {
+  const float e = uexp(-g);
+  const float d = 1.0f + e;
+  return g / d;
+}
+
+// Halving-tree sum over the 64 lanes: v[l] += v[l + off] for off = 32..1;
+// lane 0 ends with the total.  Lanes >= off read lanes past the wave, whose
+// values are never used.
+__device__ __forceinline__ float wave_tree_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_down(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ int clamp_expert(int32_t key, int E) {
+  int e = key;
+  e = e < 0 ? 0 : e;
+  return e >= E ? E - 1 : e;
+}
+
+}  // namespace uocr

@@ -1,0 +1,123 @@
+// Internal launch interface between the C-ABI entry points (uocr_moe.cpp) and
+// the kernel translation units.  Not part of the public header.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace uocr {
+
+// Elements per chunk of the bf16 chains (the int8 chains use the quant group).
+constexpr int kChunk = 128;
+
+enum WKind : int {
+  kInt8Rows = 0,      // routed int8 stack [E, N, K] + fp32 scales [E, N, K/G]
+  kBf16Rows = 1,      // routed bf16 stack [E, N, K]
+  kBf16KBlocked = 2,  // dense bf16 weight K-blocked [K/16, N, 16]
+};
+
+struct Proj {
+  const void* w;
+  const float* s;
+};
+
+// Rows grouped by the expert they read.  n_groups == nullptr means one group
+// of `identity` rows 0..identity-1 reading expert 0 (a dense weight).
+struct Rows {
+  const int32_t* n_groups;
+  const int32_t* group_expert;
+  const int32_t* group_start;
+  const int32_t* group_rows;
+  int identity;
+};
+
+struct GemvArgs {
+  float* out;
+  int64_t ldo;
+  const float* x;
+  int64_t ldx;
+  int x_div;  // activation row of output row r is r / x_div
+  Proj p[2];
+  WKind kind;
+  int E, N, K;
+  int gsize;    // int8: quant group size; bf16: 128
+  int nchunks;  // K / gsize (int8) or ceil(K / 128) (bf16)
+  int vec;      // 16-byte weight loads allowed
+  int batch;    // chunks per LDS batch (<= kGemvMaxBatch / nproj * 2)
+  Rows rows;
+};
+
+// Waves per GEMV workgroup are at most 10 (640 threads: 168 VGPRs a lane);
+// an LDS batch holds up to 16 chunks x 2 projections x 8 rows of partials.
+constexpr int kGemvMaxWaves = 10;
+constexpr int kGemvMaxThreads = kGemvMaxWaves * 64;
+constexpr int kGemvMaxBatch = 16;
+
+int gemv_workgroups(const GemvArgs& a, int max_groups);
+size_t gemv_lds_bytes(int batch, int nproj);
+hipError_t launch_gemv(const GemvArgs& a, int max_groups, int nproj, int waves, hipStream_t s);
+hipError_t launch_gemv_pair(const GemvArgs& routed, int max_groups, const GemvArgs& shared, int nproj,
+                            int waves, hipStream_t s);
+
+// ---- routing (route.hip) ----
+
+// logits[t*E + e] = dot(x[t], router[e]) in the 64-lane tree order.
+hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E,
+                         int H, hipStream_t s);
+// Softmax + top-k per token (one wave per token).  ids32/ids64/wts may be null.
+hipError_t launch_softmax_topk(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
+                               int64_t* ids64, float* wts, hipStream_t s);
+
+struct GroupTables {
+  int32_t* n_groups;      // [1]
+  int32_t* group_expert;  // [E]
+  int32_t* group_start;   // [E + 1]
+  int32_t* group_rows;    // [R]
+  int32_t* tile_start;    // [E + 1] prefix of ceil(count / bm), may be null
+  int32_t* inv;           // [R] position of row r in group_rows, may be null
+};
+// Groups R rows by their clamped expert id (ascending expert).
+hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s);
+// Decode-size routing in one workgroup: softmax + top-k of T <= 64 tokens, then
+// the grouping of their T*topk rows.
+hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
+                              float* wts, const GroupTables& g, hipStream_t s);
+
+// out[t, n] = fma-chain over j of wts[t*k+j] * y[row(t*k+j), n] from 0, + shared[t, n].
+// row(i) = inv ? inv[i] : i.  shared may be null.
+hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* wts, const int32_t* inv,
+                          const float* shared, int T, int H, int topk, hipStream_t s);
+
+// ---- int8 dequantisation and the prefill grouped GEMM (gemm.hip) ----
+
+hipError_t launch_dequant(void* out, int out_f32, const int8_t* w, const float* scales, const int32_t* idx,
+                          int E, int N, int K, int groups, int vec, hipStream_t s);
+
+struct GemmProblem {
+  // A operand: rows of x (fp32, gathered) or h (bf16, packed in group order).
+  const float* x;        // fp32 activations [T, K] (gate/up)
+  int64_t ldx;
+  const uint16_t* hb;    // bf16 activations [rows, K] (down), used when x == null
+  int64_t ldh;
+  int x_div;             // activation row of routed row r is r / x_div
+  // B operand(s)
+  Proj p[2];
+  WKind kind;
+  int N, K, groups;
+  // rows
+  Rows rows;
+  const int32_t* tile_start;  // [max_groups + 1] m-tile prefix (routed), null for dense
+  int max_groups;
+  int M;                      // dense rows (identity)
+  // output
+  int swiglu;                 // 1: out is bf16 silu(g)*u, row = position; 0: fp32
+  uint16_t* outb;
+  float* outf;
+  int64_t ldo;
+  int out_by_position;        // 1: output row = position in group order, 0: row id
+};
+hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles,
+                            hipStream_t s);
+
+}  // namespace uocr

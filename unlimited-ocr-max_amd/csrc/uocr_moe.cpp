@@ -1,0 +1,577 @@
+// Host side of the C ABI (include/uocr_moe.h): the reference's host-side shape
+// checks with its messages, workspace carving, and the launch sequences of the
+// ops and of the MoE layer (decode and prefill).
+#include "../../include/uocr_moe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "uocr_kernels.h"
+
+namespace uocr {
+int gemm_bm();
+int gemm_bn();
+int gemm_bk();
+}  // namespace uocr
+
+using namespace uocr;
+
+namespace {
+
+int fail(char* err, size_t errlen, const char* fmt, ...) {
+  if (err != nullptr && errlen > 0) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+  }
+  return 1;
+}
+
+int hip_fail(char* err, size_t errlen, const char* op, hipError_t e) {
+  return fail(err, errlen, "%s: HIP error %d (%s)", op, (int)e, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ------------------------------------------------------------------ workspace
+
+struct Carve {
+  char* base;
+  size_t off = 0;
+  explicit Carve(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t count) {
+    off = (off + 255) & ~size_t(255);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+struct CachedBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, CachedBuffer> g_ws;
+
+// The library's own workspace for (current device, stream), at least `bytes`.
+hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  CachedBuffer& b = g_ws[{dev, stream}];
+  if (b.bytes < bytes) {
+    if (b.ptr != nullptr) {
+      e = hipStreamSynchronize(stream);  // work still queued may use the old buffer
+      if (e != hipSuccess) return e;
+      (void)hipFree(b.ptr);
+      b.ptr = nullptr;
+      b.bytes = 0;
+    }
+    const size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    e = hipMalloc(&b.ptr, grow);
+    if (e != hipSuccess) return e;
+    b.bytes = grow;
+  }
+  *out = b.ptr;
+  return hipSuccess;
+}
+
+// Resolves the workspace of a call: the caller's (checked for size) or ours.
+int resolve_workspace(const char* op, void* workspace, size_t workspace_bytes, size_t need, hipStream_t stream,
+                      void** out, char* err, size_t errlen) {
+  if (workspace != nullptr) {
+    if (workspace_bytes < need)
+      return fail(err, errlen, "%s: workspace of %zu bytes is smaller than the %zu needed", op, workspace_bytes,
+                  need);
+    *out = workspace;
+    return 0;
+  }
+  const hipError_t e = own_workspace(stream, need, out);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+// Waves of a GEMV workgroup: every chunk of the batch in flight at once when
+// it fits, else the fewest waves that split the chunks evenly.
+int waves_for(int nchunks) {
+  if (nchunks < 1) return 1;
+  const int rounds = (nchunks + kGemvMaxWaves - 1) / kGemvMaxWaves;
+  return (nchunks + rounds - 1) / rounds;
+}
+
+int batch_for(int nchunks) { return nchunks < kGemvMaxBatch ? (nchunks < 1 ? 1 : nchunks) : kGemvMaxBatch; }
+
+GroupTables carve_tables(Carve& c, int E, int R, bool tiles, bool inv) {
+  GroupTables g{};
+  g.n_groups = c.take<int32_t>(1);
+  g.group_expert = c.take<int32_t>(E);
+  g.group_start = c.take<int32_t>(E + 1);
+  g.group_rows = c.take<int32_t>(R > 0 ? R : 1);
+  g.tile_start = tiles ? c.take<int32_t>(E + 1) : nullptr;
+  g.inv = inv ? c.take<int32_t>(R > 0 ? R : 1) : nullptr;
+  return g;
+}
+
+Rows rows_of(const GroupTables& g) { return Rows{g.n_groups, g.group_expert, g.group_start, g.group_rows, 0}; }
+
+// ------------------------------------------------------------------ the routed qmv ops
+
+int routed_qmv(const char* op, WKind kind, float* result, const float* x, const int32_t* ids, const void* w,
+               const float* scales, int64_t k, int64_t E, int64_t N, int64_t K, int64_t groups, hipStream_t s,
+               char* err, size_t errlen) {
+  if (k == 0 || N == 0) return 0;
+  if (E > 1024) return fail(err, errlen, "%s: more than 1024 experts are not supported", op);
+  if (k > (int64_t)1 << 30 || N > (int64_t)1 << 30 || K > (int64_t)1 << 30)
+    return fail(err, errlen, "%s: dimensions beyond 2^30 are not supported", op);
+  const int max_groups = (int)(E < k ? E : k);
+  Carve dry(nullptr);
+  carve_tables(dry, (int)E, (int)k, false, false);
+  void* ws = nullptr;
+  if (resolve_workspace(op, nullptr, 0, dry.off, s, &ws, err, errlen)) return 1;
+  Carve c(ws);
+  const GroupTables g = carve_tables(c, (int)E, (int)k, false, false);
+  hipError_t e = launch_group(ids, (int)k, (int)E, 1, g, s);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+
+  GemvArgs a{};
+  a.out = result;
+  a.ldo = N;
+  a.x = x;
+  a.ldx = K;
+  a.x_div = 1;
+  a.p[0] = Proj{w, scales};
+  a.kind = kind;
+  a.E = (int)E;
+  a.N = (int)N;
+  a.K = (int)K;
+  if (kind == kInt8Rows) {
+    a.gsize = (int)(K / groups);
+    a.nchunks = (int)groups;
+    a.vec = (K % 16 == 0) && (a.gsize % 16 == 0) && aligned16(w);
+  } else {
+    a.gsize = kChunk;
+    a.nchunks = (int)((K + kChunk - 1) / kChunk);
+    a.vec = (K % 8 == 0) && aligned16(w);
+  }
+  a.batch = batch_for(a.nchunks);
+  a.rows = rows_of(g);
+  e = launch_gemv(a, max_groups, 1, waves_for(a.batch), s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+}  // namespace
+
+extern "C" {
+
+int uocr_moe_abi_version(void) { return UOCR_MOE_ABI_VERSION; }
+
+int uocr_moe_int8_qmv(float* result, int64_t result_k, int64_t result_n, const float* x, int64_t x_k,
+                      int64_t x_kdim, const int32_t* expert_ids, int64_t ids_k, const int8_t* w, int64_t w_e,
+                      int64_t w_n, int64_t w_kdim, const float* scales, int64_t s_e, int64_t s_n, int64_t s_groups,
+                      void* stream, char* err, size_t errlen) {
+  // unlimited_ocr_max/kernels/moe_int8.mojo:194-210
+  if (x_k != result_k) return fail(err, errlen, "moe_int8_qmv: x and output disagree on k");
+  if (ids_k != result_k) return fail(err, errlen, "moe_int8_qmv: expert_ids and output disagree on k");
+  if (w_n != result_n) return fail(err, errlen, "moe_int8_qmv: w and output disagree on N");
+  if (w_kdim != x_kdim) return fail(err, errlen, "moe_int8_qmv: w and x disagree on K");
+  if (w_e < 1) return fail(err, errlen, "moe_int8_qmv: the expert stack is empty");
+  if (s_e != w_e) return fail(err, errlen, "moe_int8_qmv: scales and w disagree on E");
+  if (s_n != w_n) return fail(err, errlen, "moe_int8_qmv: scales and w disagree on N");
+  if (s_groups < 1 || w_kdim % s_groups != 0)
+    return fail(err, errlen, "moe_int8_qmv: K must be a multiple of the group count");
+  return routed_qmv("moe_int8_qmv", kInt8Rows, result, x, expert_ids, w, scales, result_k, w_e, w_n, w_kdim,
+                    s_groups, (hipStream_t)stream, err, errlen);
+}
+
+int uocr_moe_bf16_qmv(float* result, int64_t result_k, int64_t result_n, const float* x, int64_t x_k,
+                      int64_t x_kdim, const int32_t* expert_ids, int64_t ids_k, const uint16_t* w, int64_t w_e,
+                      int64_t w_n, int64_t w_kdim, void* stream, char* err, size_t errlen) {
+  // unlimited_ocr_max/kernels/moe_bf16.mojo:276-285
+  if (x_k != result_k) return fail(err, errlen, "moe_bf16_qmv: x and output disagree on k");
+  if (ids_k != result_k) return fail(err, errlen, "moe_bf16_qmv: expert_ids and output disagree on k");
+  if (w_n != result_n) return fail(err, errlen, "moe_bf16_qmv: w and output disagree on N");
+  if (w_kdim != x_kdim) return fail(err, errlen, "moe_bf16_qmv: w and x disagree on K");
+  if (w_e < 1) return fail(err, errlen, "moe_bf16_qmv: the expert stack is empty");
+  return routed_qmv("moe_bf16_qmv", kBf16Rows, result, x, expert_ids, w, nullptr, result_k, w_e, w_n, w_kdim, 1,
+                    (hipStream_t)stream, err, errlen);
+}
+
+int uocr_int8_dequant_expert(void* result, int64_t result_n, int64_t result_kdim, int result_f32, const int8_t* w,
+                             int64_t w_e, int64_t w_n, int64_t w_kdim, const float* scales, int64_t s_e,
+                             int64_t s_n, int64_t s_groups, const int32_t* expert_idx, int64_t idx_len,
+                             void* stream, char* err, size_t errlen) {
+  // unlimited_ocr_max/kernels/moe_int8.mojo:280-296
+  if (w_n != result_n) return fail(err, errlen, "int8_dequant_expert: w and output disagree on N");
+  if (w_kdim != result_kdim) return fail(err, errlen, "int8_dequant_expert: w and output disagree on K");
+  if (w_e < 1) return fail(err, errlen, "int8_dequant_expert: the expert stack is empty");
+  if (s_e != w_e) return fail(err, errlen, "int8_dequant_expert: scales and w disagree on E");
+  if (s_n != w_n) return fail(err, errlen, "int8_dequant_expert: scales and w disagree on N");
+  if (idx_len != 1) return fail(err, errlen, "int8_dequant_expert: `expert_idx` must be a single int32");
+  if (s_groups < 1 || w_kdim % s_groups != 0)
+    return fail(err, errlen, "int8_dequant_expert: K must be a multiple of the group count");
+  if (w_n * w_kdim > ((int64_t)1 << 40)) return fail(err, errlen, "int8_dequant_expert: the expert is too large");
+  const int vec = (w_kdim % 8 == 0) && aligned16(w) && aligned16(result);
+  const hipError_t e = launch_dequant(result, result_f32, w, scales, expert_idx, (int)w_e, (int)w_n, (int)w_kdim,
+                                      (int)s_groups, vec, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, "int8_dequant_expert", e);
+}
+
+int uocr_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n, const float* x, int64_t x_m,
+                        int64_t x_kdim, const uint16_t* w, int64_t w_blocks, int64_t w_n, int64_t w_kblock,
+                        int64_t tile, void* stream, char* err, size_t errlen) {
+  // unlimited_ocr_max/kernels/dense_bf16.mojo:130-144
+  if (tile < 1) return fail(err, errlen, "dense_bf16_qmv: tile must be >= 1");
+  if (result_m != x_m) return fail(err, errlen, "dense_bf16_qmv: x and output disagree on M");
+  if (w_n != result_n) return fail(err, errlen, "dense_bf16_qmv: w and output disagree on N");
+  if (w_kblock != 16) return fail(err, errlen, "dense_bf16_qmv: w is not K-blocked by KBLOCK");
+  if (w_blocks * 16 != x_kdim) return fail(err, errlen, "dense_bf16_qmv: w and x disagree on K");
+  if (x_m == 0 || result_n == 0) return 0;
+  GemvArgs a{};
+  a.out = result;
+  a.ldo = result_n;
+  a.x = x;
+  a.ldx = x_kdim;
+  a.x_div = 1;
+  a.p[0] = Proj{w, nullptr};
+  a.kind = kBf16KBlocked;
+  a.E = 1;
+  a.N = (int)result_n;
+  a.K = (int)x_kdim;
+  a.gsize = kChunk;
+  a.nchunks = (int)((x_kdim + kChunk - 1) / kChunk);
+  a.vec = aligned16(w);
+  a.batch = batch_for(a.nchunks);
+  a.rows = Rows{nullptr, nullptr, nullptr, nullptr, (int)x_m};
+  const hipError_t e = launch_gemv(a, 1, 1, waves_for(a.batch), (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, "dense_bf16_qmv", e);
+}
+
+// ------------------------------------------------------------------ the MoE block
+
+static int check_layer(const char* op, const uocr_moe_layer* L, int64_t hidden, char* err, size_t errlen) {
+  if (L == nullptr) return fail(err, errlen, "%s: no layer", op);
+  if (L->num_experts < 1 || L->num_experts > 64) return fail(err, errlen, "%s: num_experts must be in [1, 64]", op);
+  if (L->top_k < 1 || L->top_k > L->num_experts)
+    return fail(err, errlen, "%s: top_k must be in [1, num_experts]", op);
+  if (hidden != L->hidden) return fail(err, errlen, "%s: x and the layer disagree on hidden", op);
+  if (L->hidden < 16 || L->hidden % 16 || L->shared_ffn < 16 || L->shared_ffn % 16 || L->ffn < 1)
+    return fail(err, errlen, "%s: hidden and shared_ffn must be positive multiples of 16", op);
+  if (L->int8 && (L->group < 1 || L->hidden % L->group || L->ffn % L->group))
+    return fail(err, errlen, "%s: hidden and ffn must be multiples of the int8 group", op);
+  if (!L->router || !L->gate_proj || !L->up_proj || !L->down_proj || !L->shared_gate || !L->shared_up ||
+      !L->shared_down)
+    return fail(err, errlen, "%s: a layer weight is missing", op);
+  if (L->int8 && (!L->gate_proj_scales || !L->up_proj_scales || !L->down_proj_scales))
+    return fail(err, errlen, "%s: an int8 layer needs its scales", op);
+  return 0;
+}
+
+struct DecodeBufs {
+  float* logits;
+  int32_t* ids;
+  float* wts;
+  GroupTables g;
+  float* h;
+  float* hs;
+  float* y;
+  float* sh;
+};
+
+static DecodeBufs carve_decode(Carve& c, const uocr_moe_layer* L, int64_t B) {
+  const int64_t R = B * L->top_k;
+  DecodeBufs d{};
+  d.logits = c.take<float>(B * L->num_experts);
+  d.ids = c.take<int32_t>(R);
+  d.wts = c.take<float>(R);
+  d.g = carve_tables(c, (int)L->num_experts, (int)R, false, false);
+  d.h = c.take<float>(R * L->ffn);
+  d.hs = c.take<float>(B * L->shared_ffn);
+  d.y = c.take<float>(R * L->hidden);
+  d.sh = c.take<float>(B * L->hidden);
+  return d;
+}
+
+struct PrefillBufs {
+  float* logits;
+  int32_t* ids;
+  float* wts;
+  GroupTables g;
+  uint16_t* hb;
+  uint16_t* hsb;
+  float* y;
+  float* sh;
+};
+
+static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
+  const int64_t R = T * L->top_k;
+  PrefillBufs d{};
+  d.logits = c.take<float>(T * L->num_experts);
+  d.ids = c.take<int32_t>(R);
+  d.wts = c.take<float>(R);
+  d.g = carve_tables(c, (int)L->num_experts, (int)R, true, true);
+  d.hb = c.take<uint16_t>(R * L->ffn);
+  d.hsb = c.take<uint16_t>(T * L->shared_ffn);
+  d.y = c.take<float>(R * L->hidden);
+  d.sh = c.take<float>(T * L->hidden);
+  return d;
+}
+
+size_t uocr_moe_workspace_bytes(const uocr_moe_layer* layer, int64_t rows, int prefill) {
+  if (layer == nullptr || rows < 0) return 0;
+  Carve c(nullptr);
+  if (prefill)
+    carve_prefill(c, layer, rows);
+  else
+    carve_decode(c, layer, rows);
+  return c.off + 256;
+}
+
+int uocr_moe_gate(int64_t* indices, float* weights, const float* x, int64_t seq, int64_t hidden,
+                  const float* router, int64_t num_experts, int64_t top_k, int renormalize, void* workspace,
+                  size_t workspace_bytes, void* stream, char* err, size_t errlen) {
+  const char* op = "uocr_moe_gate";
+  if (num_experts < 1 || num_experts > 64) return fail(err, errlen, "%s: num_experts must be in [1, 64]", op);
+  if (top_k < 1 || top_k > num_experts) return fail(err, errlen, "%s: top_k must be in [1, num_experts]", op);
+  if (seq < 0 || hidden < 1) return fail(err, errlen, "%s: bad x shape", op);
+  if (seq == 0) return 0;
+  const hipStream_t s = (hipStream_t)stream;
+  void* ws = nullptr;
+  if (resolve_workspace(op, workspace, workspace_bytes, (size_t)(seq * num_experts) * sizeof(float) + 256, s, &ws,
+                        err, errlen))
+    return 1;
+  float* logits = static_cast<float*>(ws);
+  hipError_t e = launch_logits(logits, x, hidden, router, (int)seq, (int)num_experts, (int)hidden, s);
+  if (e == hipSuccess)
+    e = launch_softmax_topk(logits, (int)seq, (int)num_experts, (int)top_k, renormalize, nullptr, indices, weights,
+                            s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidden, const uocr_moe_layer* L,
+                         int32_t* expert_ids, float* expert_weights, void* workspace, size_t workspace_bytes,
+                         void* stream, char* err, size_t errlen) {
+  const char* op = "uocr_moe_decode_rows";
+  if (check_layer(op, L, hidden, err, errlen)) return 1;
+  if (rows < 0 || rows > 64) return fail(err, errlen, "%s: rows must be in [0, 64]", op);
+  if (rows == 0) return 0;
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t B = rows, R = rows * L->top_k;
+  Carve dry(nullptr);
+  carve_decode(dry, L, B);
+  void* ws = nullptr;
+  if (resolve_workspace(op, workspace, workspace_bytes, dry.off, s, &ws, err, errlen)) return 1;
+  Carve c(ws);
+  const DecodeBufs d = carve_decode(c, L, B);
+  const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
+  const int max_groups = (int)(E < R ? E : R);
+
+  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)B, E, H, s);
+  if (e == hipSuccess) e = launch_route_small(d.logits, (int)B, E, (int)L->top_k, L->renormalize, d.ids, d.wts, d.g, s);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+
+  // gate/up (+ SwiGLU) for the routed rows and the shared experts
+  GemvArgs gu{};
+  gu.out = d.h;
+  gu.ldo = F;
+  gu.x = x;
+  gu.ldx = H;
+  gu.x_div = (int)L->top_k;
+  gu.kind = L->int8 ? kInt8Rows : kBf16Rows;
+  gu.p[0] = Proj{L->gate_proj, L->gate_proj_scales};
+  gu.p[1] = Proj{L->up_proj, L->up_proj_scales};
+  gu.E = E;
+  gu.N = F;
+  gu.K = H;
+  if (L->int8) {
+    gu.gsize = (int)L->group;
+    gu.nchunks = H / (int)L->group;
+    gu.vec = (H % 16 == 0) && (gu.gsize % 16 == 0) && aligned16(L->gate_proj) && aligned16(L->up_proj);
+  } else {
+    gu.gsize = kChunk;
+    gu.nchunks = (H + kChunk - 1) / kChunk;
+    gu.vec = (H % 8 == 0) && aligned16(L->gate_proj) && aligned16(L->up_proj);
+  }
+  gu.batch = batch_for(gu.nchunks);
+  gu.rows = rows_of(d.g);
+
+  GemvArgs sgu{};
+  sgu.out = d.hs;
+  sgu.ldo = Fs;
+  sgu.x = x;
+  sgu.ldx = H;
+  sgu.x_div = 1;
+  sgu.kind = kBf16KBlocked;
+  sgu.p[0] = Proj{L->shared_gate, nullptr};
+  sgu.p[1] = Proj{L->shared_up, nullptr};
+  sgu.E = 1;
+  sgu.N = Fs;
+  sgu.K = H;
+  sgu.gsize = kChunk;
+  sgu.nchunks = (H + kChunk - 1) / kChunk;
+  sgu.vec = aligned16(L->shared_gate) && aligned16(L->shared_up);
+  sgu.batch = batch_for(sgu.nchunks);
+  sgu.rows = Rows{nullptr, nullptr, nullptr, nullptr, (int)B};
+  const int w1 = waves_for(gu.batch > sgu.batch ? gu.batch : sgu.batch);
+  e = launch_gemv_pair(gu, max_groups, sgu, 2, w1, s);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+
+  // down for the routed rows and the shared experts
+  GemvArgs dn = gu;
+  dn.out = d.y;
+  dn.ldo = H;
+  dn.x = d.h;
+  dn.ldx = F;
+  dn.x_div = 1;
+  dn.p[0] = Proj{L->down_proj, L->down_proj_scales};
+  dn.p[1] = Proj{nullptr, nullptr};
+  dn.N = H;
+  dn.K = F;
+  if (L->int8) {
+    dn.nchunks = F / (int)L->group;
+    dn.vec = (F % 16 == 0) && (dn.gsize % 16 == 0) && aligned16(L->down_proj);
+  } else {
+    dn.nchunks = (F + kChunk - 1) / kChunk;
+    dn.vec = (F % 8 == 0) && aligned16(L->down_proj);
+  }
+  dn.batch = batch_for(dn.nchunks);
+  GemvArgs sdn = sgu;
+  sdn.out = d.sh;
+  sdn.ldo = H;
+  sdn.x = d.hs;
+  sdn.ldx = Fs;
+  sdn.p[0] = Proj{L->shared_down, nullptr};
+  sdn.p[1] = Proj{nullptr, nullptr};
+  sdn.N = H;
+  sdn.K = Fs;
+  sdn.nchunks = (Fs + kChunk - 1) / kChunk;
+  sdn.vec = aligned16(L->shared_down);
+  sdn.batch = batch_for(sdn.nchunks);
+  const int w2 = waves_for(dn.batch > sdn.batch ? dn.batch : sdn.batch);
+  e = launch_gemv_pair(dn, max_groups, sdn, 1, w2, s);
+  if (e == hipSuccess) e = launch_combine(out, d.y, H, d.wts, nullptr, d.sh, (int)B, H, (int)L->top_k, s);
+  if (e == hipSuccess && expert_ids) e = hipMemcpyAsync(expert_ids, d.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
+  if (e == hipSuccess && expert_weights)
+    e = hipMemcpyAsync(expert_weights, d.wts, R * sizeof(float), hipMemcpyDeviceToDevice, s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, const uocr_moe_layer* L,
+                     int32_t* expert_ids, float* expert_weights, void* workspace, size_t workspace_bytes,
+                     void* stream, char* err, size_t errlen) {
+  const char* op = "uocr_moe_forward";
+  if (check_layer(op, L, hidden, err, errlen)) return 1;
+  const int BN = gemm_bn(), BK = gemm_bk(), BM = gemm_bm();
+  if (L->hidden % BN || L->ffn % BN || L->shared_ffn % BN)
+    return fail(err, errlen, "%s: hidden, ffn and shared_ffn must be multiples of %d", op, BN);
+  if (L->int8 && L->group % BK) return fail(err, errlen, "%s: the int8 group must be a multiple of %d", op, BK);
+  if (!aligned16(x) || !aligned16(L->gate_proj) || !aligned16(L->up_proj) || !aligned16(L->down_proj) ||
+      !aligned16(L->shared_gate) || !aligned16(L->shared_up) || !aligned16(L->shared_down))
+    return fail(err, errlen, "%s: x and the weights must be 16-byte aligned", op);
+  if (seq < 0 || seq * L->top_k > ((int64_t)1 << 28)) return fail(err, errlen, "%s: seq out of range", op);
+  if (seq == 0) return 0;
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t T = seq, R = seq * L->top_k;
+  Carve dry(nullptr);
+  carve_prefill(dry, L, T);
+  void* ws = nullptr;
+  if (resolve_workspace(op, workspace, workspace_bytes, dry.off, s, &ws, err, errlen)) return 1;
+  Carve c(ws);
+  const PrefillBufs d = carve_prefill(c, L, T);
+  const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
+
+  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, s);
+  if (e == hipSuccess)
+    e = launch_softmax_topk(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, nullptr, d.wts, s);
+  if (e == hipSuccess) e = launch_group(d.ids, (int)R, E, BM, d.g, s);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+  const int max_groups = (int)(E < R ? E : R);
+  const int max_mtiles = (int)((R + BM - 1) / BM) + max_groups;
+
+  GemmProblem gu{};
+  gu.x = x;
+  gu.ldx = H;
+  gu.x_div = (int)L->top_k;
+  gu.p[0] = Proj{L->gate_proj, L->gate_proj_scales};
+  gu.p[1] = Proj{L->up_proj, L->up_proj_scales};
+  gu.kind = L->int8 ? kInt8Rows : kBf16Rows;
+  gu.N = F;
+  gu.K = H;
+  gu.groups = L->int8 ? (int)(H / L->group) : 1;
+  gu.rows = rows_of(d.g);
+  gu.tile_start = d.g.tile_start;
+  gu.max_groups = max_groups;
+  gu.swiglu = 1;
+  gu.outb = d.hb;
+  gu.ldo = F;
+  gu.out_by_position = 1;
+
+  GemmProblem sgu{};
+  sgu.x = x;
+  sgu.ldx = H;
+  sgu.x_div = 1;
+  sgu.p[0] = Proj{L->shared_gate, nullptr};
+  sgu.p[1] = Proj{L->shared_up, nullptr};
+  sgu.kind = kBf16KBlocked;
+  sgu.N = Fs;
+  sgu.K = H;
+  sgu.rows = Rows{nullptr, nullptr, nullptr, nullptr, 0};
+  sgu.M = (int)T;
+  sgu.swiglu = 1;
+  sgu.outb = d.hsb;
+  sgu.ldo = Fs;
+  e = launch_gemm_pair(gu, sgu, max_mtiles, s);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+
+  GemmProblem dn = gu;
+  dn.x = nullptr;
+  dn.hb = d.hb;
+  dn.ldh = F;
+  dn.x_div = 1;
+  dn.p[0] = Proj{L->down_proj, L->down_proj_scales};
+  dn.p[1] = Proj{nullptr, nullptr};
+  dn.N = H;
+  dn.K = F;
+  dn.groups = L->int8 ? (int)(F / L->group) : 1;
+  dn.swiglu = 0;
+  dn.outb = nullptr;
+  dn.outf = d.y;
+  dn.ldo = H;
+
+  GemmProblem sdn = sgu;
+  sdn.x = nullptr;
+  sdn.hb = d.hsb;
+  sdn.ldh = Fs;
+  sdn.p[0] = Proj{L->shared_down, nullptr};
+  sdn.p[1] = Proj{nullptr, nullptr};
+  sdn.N = H;
+  sdn.K = Fs;
+  sdn.swiglu = 0;
+  sdn.outb = nullptr;
+  sdn.outf = d.sh;
+  sdn.ldo = H;
+  e = launch_gemm_pair(dn, sdn, max_mtiles, s);
+  if (e == hipSuccess) e = launch_combine(out, d.y, H, d.wts, d.g.inv, d.sh, (int)T, H, (int)L->top_k, s);
+  if (e == hipSuccess && expert_ids) e = hipMemcpyAsync(expert_ids, d.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
+  if (e == hipSuccess && expert_weights)
+    e = hipMemcpyAsync(expert_weights, d.wts, R * sizeof(float), hipMemcpyDeviceToDevice, s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+void uocr_moe_release(void) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (auto& kv : g_ws)
+    if (kv.second.ptr != nullptr) (void)hipFree(kv.second.ptr);
+  g_ws.clear();
+}
+
+}  // extern "C"

@@ -1,0 +1,33 @@
+"""uocr_moe: the DeepSeek-V2 routed-expert MoE block of unlimited-ocr-max on MI355X (gfx950).
+
+The product is the HIP library ``libuocr_moe.so`` behind a C ABI
+(``include/uocr_moe.h``); this package is its Python host side, mirroring the
+reference's op names (:mod:`uocr_moe.ops`) and MoE module (:mod:`uocr_moe.moe`).
+"""
+
+from ._lib import LIB_PATH, UocrError
+from .moe import MoE, MoeConfig, gate
+from .ops import (
+    custom,
+    dense_bf16_qmv,
+    int8_dequant_expert,
+    kblocked,
+    moe_bf16_qmv,
+    moe_int8_qmv,
+    quantize_per_group,
+)
+
+__all__ = [
+    "LIB_PATH",
+    "MoE",
+    "MoeConfig",
+    "UocrError",
+    "custom",
+    "dense_bf16_qmv",
+    "gate",
+    "int8_dequant_expert",
+    "kblocked",
+    "moe_bf16_qmv",
+    "moe_int8_qmv",
+    "quantize_per_group",
+]

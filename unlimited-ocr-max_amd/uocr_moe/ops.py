@@ -1,0 +1,178 @@
+"""The reference's custom ops on PyTorch-ROCm tensors, through the HIP library.
+
+Names, argument order, dtypes, output shapes and error messages follow the
+reference's MAX ops (``unlimited_ocr_max/kernels/*.mojo``) as its graph code
+stages them (``unlimited_ocr_max/decoder.py:166-184,325-330,355-366``):
+
+=====================  ===================================================  ==================
+op                     values                                               result
+=====================  ===================================================  ==================
+moe_int8_qmv           x f32 [k,K], expert_ids i32 [k], w i8 [E,N,K],       f32 [k,N]
+                       scales f32 [E,N,K/G]
+moe_bf16_qmv           x f32 [k,K], expert_ids i32 [k], w bf16 [E,N,K]      f32 [k,N]
+int8_dequant_expert    w i8 [E,N,K], scales f32 [E,N,K/G], expert_idx i32   bf16 (or f32) [N,K]
+                       [1]
+dense_bf16_qmv         x f32 [M,K], w bf16 [K/16,N,16]; parameter ``tile``  f32 [M,N]
+=====================  ===================================================  ==================
+
+:func:`custom` dispatches by symbol like ``ops.custom(symbol, values=...)``.
+Inputs must be GPU tensors; non-contiguous views are packed first (the
+reference reads strided inputs with the same bits as packed ones).  Work is
+enqueued on the current torch stream.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+KBLOCK = 16
+INT8_GROUP_SIZE = 128
+#: The fewest work items the reference's tile rule leaves a dense_bf16_qmv call
+#: (unlimited_ocr_max/decoder.py:141).
+DENSE_MIN_ITEMS = 2048
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _gpu(op: str, name: str, t: torch.Tensor, dtype: torch.dtype, rank: int) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{op}: {name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{op}: {name} must be {dtype}, got {t.dtype}")
+    if t.dim() != rank:
+        raise ValueError(f"{op}: {name} must be rank {rank}, got shape {tuple(t.shape)}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{op}: {name} must be on the GPU, got {t.device}")
+    return t.contiguous()
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _rows_per_read(rows: int, out_dim: int) -> int:
+    """The reference's tile rule for dense_bf16_qmv (unlimited_ocr_max/decoder.py:144-163)."""
+    tiles = 1
+    while True:
+        tile = math.ceil(rows / tiles)
+        if tile == 1 or out_dim * math.ceil(rows / tile) >= DENSE_MIN_ITEMS:
+            return tile
+        tiles += 1
+
+
+def moe_int8_qmv(x, expert_ids, w, scales, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out[s,n] = sum_g scales[e,n,g] * sum_{kk in g} f32(w[e,n,kk]) * x[s,kk]``, ``e = clamp(expert_ids[s])``.
+
+    unlimited_ocr_max/kernels/moe_int8.mojo:181-258, bitwise its operation order.
+    """
+    op = "moe_int8_qmv"
+    x = _gpu(op, "x", x, torch.float32, 2)
+    expert_ids = _gpu(op, "expert_ids", expert_ids, torch.int32, 1)
+    w = _gpu(op, "w", w, torch.int8, 3)
+    scales = _gpu(op, "scales", scales, torch.float32, 3)
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
+    out = _gpu(op, "result", out, torch.float32, 2)
+    _lib.call("uocr_moe_int8_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0], x.shape[1],
+              expert_ids.data_ptr(), expert_ids.shape[0], w.data_ptr(), *w.shape, scales.data_ptr(), *scales.shape,
+              _stream(x))
+    return out
+
+
+def moe_bf16_qmv(x, expert_ids, w, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out[s,n] = sum_kk f32(w[e,n,kk]) * x[s,kk]`` (unlimited_ocr_max/kernels/moe_bf16.mojo:264-345)."""
+    op = "moe_bf16_qmv"
+    x = _gpu(op, "x", x, torch.float32, 2)
+    expert_ids = _gpu(op, "expert_ids", expert_ids, torch.int32, 1)
+    w = _gpu(op, "w", w, torch.bfloat16, 3)
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
+    out = _gpu(op, "result", out, torch.float32, 2)
+    _lib.call("uocr_moe_bf16_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0], x.shape[1],
+              expert_ids.data_ptr(), expert_ids.shape[0], w.data_ptr(), *w.shape, _stream(x))
+    return out
+
+
+def int8_dequant_expert(w, scales, expert_idx, *, dtype: torch.dtype = torch.bfloat16,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """Expert ``clamp(expert_idx[0])`` as ``round(f32(q) * scale)`` in ``dtype`` [N, K]
+    (unlimited_ocr_max/kernels/moe_int8.mojo:261-342)."""
+    op = "int8_dequant_expert"
+    w = _gpu(op, "w", w, torch.int8, 3)
+    scales = _gpu(op, "scales", scales, torch.float32, 3)
+    expert_idx = _gpu(op, "expert_idx", expert_idx, torch.int32, 1)
+    if out is None:
+        if dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError(f"{op}: the result must be bfloat16 or float32, got {dtype}")
+        out = torch.empty((w.shape[1], w.shape[2]), dtype=dtype, device=w.device)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{op}: the result must be bfloat16 or float32, got {out.dtype}")
+    out = _gpu(op, "result", out, out.dtype, 2)
+    _lib.call("uocr_int8_dequant_expert", out.data_ptr(), out.shape[0], out.shape[1], int(out.dtype == torch.float32),
+              w.data_ptr(), *w.shape, scales.data_ptr(), *scales.shape, expert_idx.data_ptr(), expert_idx.shape[0],
+              _stream(w))
+    return out
+
+
+def dense_bf16_qmv(x, w, *, tile: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x @ W.T`` for a K-blocked bf16 ``w [K/16, N, 16]`` (unlimited_ocr_max/kernels/dense_bf16.mojo:119-158).
+
+    ``tile`` defaults to the reference's :func:`_rows_per_read`; a row's bits do not depend on it.
+    """
+    op = "dense_bf16_qmv"
+    x = _gpu(op, "x", x, torch.float32, 2)
+    w = _gpu(op, "w", w, torch.bfloat16, 3)
+    if tile is None:
+        tile = _rows_per_read(int(x.shape[0]), int(w.shape[1]))
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
+    out = _gpu(op, "result", out, torch.float32, 2)
+    _lib.call("uocr_dense_bf16_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0], x.shape[1],
+              w.data_ptr(), *w.shape, int(tile), _stream(x))
+    return out
+
+
+_OPS = {
+    "moe_int8_qmv": moe_int8_qmv,
+    "moe_bf16_qmv": moe_bf16_qmv,
+    "int8_dequant_expert": int8_dequant_expert,
+    "dense_bf16_qmv": dense_bf16_qmv,
+}
+
+
+def custom(symbol: str, values: list, out: torch.Tensor | None = None, parameters: dict | None = None) -> list:
+    """``ops.custom(symbol, values=[...])``-style dispatch; returns ``[result]``."""
+    if symbol not in _OPS:
+        raise KeyError(f"unknown custom op {symbol!r}; known: {sorted(_OPS)}")
+    kwargs = dict(parameters or {})
+    if out is not None:
+        kwargs["out"] = out
+    return [_OPS[symbol](*values, **kwargs)]
+
+
+def kblocked(weight: torch.Tensor) -> torch.Tensor:
+    """``W [N, K]`` as ``[K/16, N, 16]`` (unlimited_ocr_max/weight_adapters.py:222-233)."""
+    n, k = weight.shape
+    if k % KBLOCK:
+        raise ValueError(f"a K-blocked projection needs K to be a multiple of {KBLOCK}, got shape {tuple(weight.shape)}")
+    return weight.reshape(n, k // KBLOCK, KBLOCK).permute(1, 0, 2).contiguous()
+
+
+def quantize_per_group(w: torch.Tensor, group: int = INT8_GROUP_SIZE) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-group int8 of ``[..., K]`` along K (tools/quantize_int8.py:54-70,298-329):
+    ``scale = amax/127`` (1.0 for an all-zero group), ``q = clip(rint(w/scale), -127, 127)``, in fp32."""
+    wf = w.float()
+    k = wf.shape[-1]
+    if k % group:
+        raise ValueError(f"K={k} is not divisible by the group size {group}")
+    grouped = wf.reshape(*wf.shape[:-1], k // group, group)
+    amax = grouped.abs().amax(dim=-1)
+    scales = torch.where(amax == 0, torch.ones_like(amax), amax / 127.0)
+    q = torch.round(grouped / scales[..., None]).clamp_(-127, 127)
+    return q.to(torch.int8).reshape(wf.shape).contiguous(), scales.contiguous()
