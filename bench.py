@@ -1,0 +1,425 @@
+#!/usr/bin/env python3
+"""Benchmark of the DeepSeek-V2 routed-expert MoE block on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): one int8 MoE
+layer -- hidden 1280, 64 routed SwiGLU experts of width 896 (int8, fp32 scales
+per 128-group along K), top-6 softmax gate, 2 shared bf16 experts (width 1792),
+fp32 router -- at decode batch 1 and batch 8, on synthetic data: weights
+N(0, 0.02) rounded to bf16 then quantised, hidden states RMSNorm(N(0, 1)).
+
+Cold HBM: the timed steps rotate over 11 independently seeded layers (2.65 GB
+of int8 stacks, the 11-layer decode stack) and over distinct token batches,
+so the working set is far beyond the 256 MB Infinity Cache; a "warm" figure
+repeats one layer and one batch.  A step is one MoE layer over one batch.  K
+steps are captured in one HIP graph (launch-bound decode) and replayed once
+between a synchronize and a synchronize; W warm-up steps run first.
+
+Reported (one JSON line): the int8 B=1 layer's microseconds (``value``) with
+B=1/B=8 HBM-roofline fractions, the 11-layer decode step at B=8, prefill T=512
+(Zipf-skewed routing) and T=4096 (plus the adversarial all-on-experts-0..5
+case) TFLOP/s against the bf16 MFMA peak, the bf16-weight decode, per-kernel
+durations measured live with HIP events around each launch, and the CPU
+oracle's restatement of the reference's CPU path timed on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "unlimited-ocr-max_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "int8 MoE layer µs & % HBM peak at decode B=1/8; prefill T=512 TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+E, H, F, N_SHARED, TOPK, GROUP = 64, 1280, 896, 2, 6, 128
+FS = N_SHARED * F
+LAYERS = 11
+ZIPF_S = 1.1
+ZIPF_SCALE = 0.75
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------- synthetic layers
+
+
+def make_layer(seed: int, int8: bool, device: str):
+    """One layer of seeded N(0, 0.02) weights (bf16), int8-quantised per 128-group when ``int8``."""
+    import torch
+    import uocr_moe
+
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def randn(shape):
+        return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+
+    w = {"gate.gate_score.weight": randn((E, H)).float()}
+    for proj, shape in (("gate_proj", (E, F, H)), ("up_proj", (E, F, H)), ("down_proj", (E, H, F))):
+        stack = randn(shape)
+        if int8:
+            q, s = uocr_moe.quantize_per_group(stack, GROUP)
+            w[f"experts.{proj}"], w[f"experts.{proj}_scales"] = q, s
+        else:
+            w[f"experts.{proj}"] = stack
+        del stack
+    for proj, shape in (("gate_proj", (FS, H)), ("up_proj", (FS, H)), ("down_proj", (H, FS))):
+        w[f"shared_experts.{proj}.weight"] = uocr_moe.kblocked(randn(shape))
+    cfg = uocr_moe.MoeConfig(hidden_size=H, moe_intermediate_size=F, n_routed_experts=E, num_experts_per_tok=TOPK,
+                             n_shared_experts=N_SHARED, int8_experts=int8, group_size=GROUP)
+    return uocr_moe.MoE(cfg, w), w
+
+
+def rmsnorm_rows(g, rows: int, device: str):
+    import torch
+
+    x = torch.randn((rows, H), generator=g, device=device, dtype=torch.float32)
+    return (x / torch.sqrt(torch.mean(x.double() ** 2, dim=1, keepdim=True) + 1e-6).float()).contiguous()
+
+
+# ---------------------------------------------------------------------------- algorithmic work
+
+
+def expert_bytes(int8: bool) -> int:
+    if int8:
+        return 3 * F * H + 4 * (2 * F * (H // GROUP) + H * (F // GROUP))
+    return 3 * F * H * 2
+
+
+def decode_bytes(u: int, rows: int, int8: bool) -> int:
+    """Weights of the u selected experts (each read once), the shared experts, the router, x in, out."""
+    return u * expert_bytes(int8) + 3 * FS * H * 2 + E * H * 4 + 2 * rows * H * 4
+
+
+def gateup_bytes(u: int, rows: int, int8: bool) -> int:
+    """The fused gate/up launch: routed gate+up weights, shared gate+up weights, x in, h out."""
+    routed = 2 * F * H + 4 * 2 * F * (H // GROUP) if int8 else 2 * F * H * 2
+    return u * routed + 2 * FS * H * 2 + rows * H * 4 + (rows * TOPK * F + rows * FS) * 4
+
+
+def prefill_flops(T: int) -> float:
+    return 2.0 * T * TOPK * 3 * F * H + 2.0 * T * 3 * FS * H + 2.0 * T * H * E
+
+
+# ---------------------------------------------------------------------------- timing helpers
+
+
+def graph_of(fn_steps):
+    """A HIP graph of the given step callables, captured after one eager warm-up of each."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for fn in fn_steps[: min(len(fn_steps), 3)]:
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for fn in fn_steps:
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, repeats: int = 5) -> float:
+    """Median ms of one replay, each bracketed by synchronizes and timed with stream events."""
+    import torch
+
+    times = []
+    for _ in range(repeats):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(stop))
+    return statistics.median(times)
+
+
+def kernel_times(fn_steps) -> dict[str, list[float]]:
+    """Per-launch kernel durations (ms) of the steps run eagerly, by kernel name."""
+    import torch
+    from uocr_moe import _lib
+
+    cap = 16 * len(fn_steps) + 16
+    torch.cuda.synchronize()
+    _lib.timing_begin(cap)
+    for fn in fn_steps:
+        fn()
+    rows = _lib.timing_end(cap)
+    out: dict[str, list[float]] = {}
+    for name, ms in rows:
+        out.setdefault(name, []).append(ms)
+    return out
+
+
+# ---------------------------------------------------------------------------- benchmark parts
+
+
+def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: str, seed: int) -> dict:
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    pool = [rmsnorm_rows(g, B, device) for _ in range(4 * LAYERS)]
+    ws = layers[0].workspace(B, prefill=False)
+    # the experts each (layer, batch) pair selects
+    u_of = {}
+    for i, x in enumerate(pool):
+        _, ids, _ = layers[i % LAYERS].decode_rows(x, workspace=ws, routing=True)
+        u_of[i] = int(torch.unique(ids).numel())
+    plan = [(i % LAYERS, i % len(pool)) for i in range(steps)]
+    fns = [lambda l=l, p=p: layers[l].decode_rows(pool[p], workspace=ws) for l, p in plan]
+    wfns = [lambda l=l, p=p: layers[l].decode_rows(pool[p], workspace=ws) for l, p in plan[:warmup]]
+    if wfns:
+        graph_of(wfns).replay()
+    graph = graph_of(fns)
+    ms = time_graph(graph)
+    us = ms * 1e3 / steps
+    total_bytes = sum(decode_bytes(u_of[p], B, int8) for _, p in plan)
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    # warm: one layer, one batch, repeated
+    wgraph = graph_of([lambda: layers[0].decode_rows(pool[0], workspace=ws)] * min(steps, 4 * LAYERS))
+    warm_us = time_graph(wgraph) * 1e3 / min(steps, 4 * LAYERS)
+    warm_gbs = decode_bytes(u_of[0], B, int8) / (warm_us * 1e-6) / 1e9
+    # live per-kernel durations over one rotation (eager; events around each launch)
+    kt = kernel_times([lambda l=l, p=p: layers[l].decode_rows(pool[p], workspace=ws) for l, p in plan[: 4 * LAYERS]])
+    gu = kt.get("gemv_gateup", [])
+    gu_bytes = [gateup_bytes(u_of[p], B, int8) for _, p in plan[: len(gu)]]
+    res = {
+        "us_per_layer": round(us, 3),
+        "tokens_per_s": round(B / (us * 1e-6), 1),
+        "bytes_per_layer_avg": int(total_bytes / steps),
+        "distinct_experts_avg": round(statistics.mean(u_of[p] for _, p in plan), 2),
+        "hbm_gbs": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "warm_us_per_layer": round(warm_us, 3),
+        "warm_gbs": round(warm_gbs, 1),
+        "kernels_us_avg": {k: round(1e3 * statistics.mean(v), 3) for k, v in kt.items()},
+        "kernel_sum_us_avg": round(1e3 * sum(sum(v) for v in kt.values()) / (4 * LAYERS), 3),
+    }
+    if gu:
+        res["gateup_kernel"] = {
+            "launches": len(gu),
+            "avg_us": round(1e3 * statistics.mean(gu), 3),
+            "avg_bytes": int(statistics.mean(gu_bytes)),
+            "gbs": round(sum(gu_bytes) / (sum(gu) * 1e-3) / 1e9, 1),
+        }
+    return res
+
+
+def zipf_prefill_inputs(g, T: int, device: str, seed: int):
+    """274 vision + 238 text rows of N(0,1) (per 512); a constant feature carries a Zipf(1.1) expert bias."""
+    import torch
+
+    x = torch.randn((T, H), generator=g, device=device, dtype=torch.float32)
+    x[:, 0] = 1.0
+    ranks = torch.randperm(E, generator=torch.Generator().manual_seed(seed)).double() + 1.0
+    bias = (ZIPF_SCALE * -ZIPF_S * torch.log(ranks)).float().to(device)
+    return x.contiguous(), bias
+
+
+def bench_prefill(layers_w, T: int, device: str, seed: int, adversarial: bool = False) -> dict:
+    import torch
+    import uocr_moe
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    x, bias = zipf_prefill_inputs(g, T, device, seed)
+    if adversarial:
+        bias = torch.zeros(E, device=device)
+        bias[:6] = 10.0
+    moes = []
+    for moe, w in layers_w:
+        r = w["gate.gate_score.weight"].clone()
+        r[:, 0] = bias
+        moes.append(uocr_moe.MoE(moe.config, {**w, "gate.gate_score.weight": r}))
+    ws = moes[0].workspace(T, prefill=True)
+    hist = None
+    touched = []
+    for m in moes:
+        _, ids, _ = m(x, workspace=ws, routing=True)
+        counts = torch.bincount(ids.flatten().long(), minlength=E)
+        touched.append(int((counts > 0).sum()))
+        if hist is None:
+            hist = counts.cpu().tolist()
+    fns = [lambda m=m: m(x, workspace=ws) for m in moes]
+    graph = graph_of(fns)
+    ms = time_graph(graph, repeats=5)
+    us = ms * 1e3 / len(moes)
+    flops = prefill_flops(T)
+    tflops = flops / (us * 1e-6) / 1e12
+    bytes_ = statistics.mean(t * expert_bytes(True) for t in touched) + 3 * FS * H * 2 + E * H * 4 + 2 * T * H * 4
+    t_hbm = bytes_ / (HBM_PEAK_GBS * 1e9)
+    t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12)
+    kt = kernel_times(fns)
+    return {
+        "tokens": T,
+        "us_per_layer": round(us, 2),
+        "tokens_per_s": round(T / (us * 1e-6), 1),
+        "gflop": round(flops / 1e9, 3),
+        "tflops": round(tflops, 2),
+        "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+        "bytes_per_layer": int(bytes_),
+        "hbm_gbs": round(bytes_ / (us * 1e-6) / 1e9, 1),
+        "roofline_bound": "hbm" if t_hbm > t_mfma else "mfma",
+        "roofline_frac": round(max(t_hbm, t_mfma) / (us * 1e-6), 4),
+        "experts_touched_avg": round(statistics.mean(touched), 2),
+        "expert_histogram_layer0": hist,
+        "kernels_us_avg": {k: round(1e3 * statistics.mean(v), 2) for k, v in kt.items()},
+    }
+
+
+def bench_cpu_baseline(layer_w, budget_s: float) -> dict:
+    """The reference's CPU decomposition (the oracle's restatement) on this host: int8 layer, B=1 and B=8."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    def host(t):
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).cpu().numpy().view(np.uint16)
+        return t.cpu().numpy()
+
+    w = {k: host(v) for k, v in layer_w.items()}
+    layer = O.MoeWeights(router=w["gate.gate_score.weight"], gate=w["experts.gate_proj"], up=w["experts.up_proj"],
+                         down=w["experts.down_proj"], gate_s=w["experts.gate_proj_scales"],
+                         up_s=w["experts.up_proj_scales"], down_s=w["experts.down_proj_scales"],
+                         sh_gate=w["shared_experts.gate_proj.weight"], sh_up=w["shared_experts.up_proj.weight"],
+                         sh_down=w["shared_experts.down_proj.weight"], topk=TOPK, group=GROUP)
+    rng = np.random.default_rng(5)
+    cores = O.threads(0)
+    out = {"cores": cores}
+    for B in (1, 8):
+        x = O.rmsnorm_rows(rng, B, H)
+        O.moe_decode_refdecomp(x, layer, threads=cores)  # warm-up
+        times = []
+        t_end = time.perf_counter() + budget_s / 2
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            O.moe_decode_refdecomp(x, layer, threads=cores)
+            times.append(time.perf_counter() - t0)
+        out[f"b{B}_us"] = round(1e6 * statistics.median(times), 1)
+        out[f"b{B}_runs"] = len(times)
+    return out
+
+
+# ---------------------------------------------------------------------------- main
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=440, help="timed decode layer-steps (one graph replay)")
+    ap.add_argument("--warmup", type=int, default=44)
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline sampling")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="decode only (no prefill, no bf16)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the MoE block runs on a single MI355X here "
+              "(run with --gpus 1; multi-GPU sharding is not part of this build)", file=sys.stderr)
+        return 2
+    if args.steps < 1:
+        print("--steps must be >= 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = "cuda:0"
+    t_start = time.perf_counter()
+    log(f"device {torch.cuda.get_device_name(0)}; building {LAYERS} int8 layers")
+    layers_w = [make_layer(1000 + l, True, dev) for l in range(LAYERS)]
+    layers = [m for m, _ in layers_w]
+    torch.cuda.synchronize()
+    results: dict = {}
+    log("decode int8 B=1")
+    results["decode_int8_b1"] = bench_decode(layers, 1, args.steps, args.warmup, True, dev, 1)
+    log(f"  {results['decode_int8_b1']['us_per_layer']} us/layer")
+    log("decode int8 B=8")
+    results["decode_int8_b8"] = bench_decode(layers, 8, args.steps, args.warmup, True, dev, 8)
+    log(f"  {results['decode_int8_b8']['us_per_layer']} us/layer")
+    us8 = results["decode_int8_b8"]["us_per_layer"]
+    results["decode_int8_11layer_step_b8"] = {"us_per_step": round(11 * us8, 2),
+                                              "tokens_per_s": round(8 / (11 * us8 * 1e-6), 1)}
+    if not args.quick:
+        log("prefill int8 T=512 (Zipf)")
+        results["prefill_int8_t512"] = bench_prefill(layers_w, 512, dev, 512)
+        log(f"  {results['prefill_int8_t512']['tflops']} TFLOP/s")
+        log("prefill int8 T=4096")
+        results["prefill_int8_t4096"] = bench_prefill(layers_w[:4], 4096, dev, 4096)
+        results["prefill_int8_t4096_adversarial"] = bench_prefill(layers_w[:4], 4096, dev, 4097, adversarial=True)
+        log(f"  {results['prefill_int8_t4096']['tflops']} / {results['prefill_int8_t4096_adversarial']['tflops']} TFLOP/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = bench_cpu_baseline(layers_w[0][1], args.cpu_budget)
+    if not args.quick:
+        del layers_w, layers
+        torch.cuda.empty_cache()
+        log("decode bf16 B=1/8")
+        bf = [make_layer(2000 + l, False, dev)[0] for l in range(LAYERS)]
+        results["decode_bf16_b1"] = bench_decode(bf, 1, args.steps, args.warmup, False, dev, 101)
+        results["decode_bf16_b8"] = bench_decode(bf, 8, args.steps, args.warmup, False, dev, 108)
+        del bf
+
+    b1 = results["decode_int8_b1"]
+    gu = b1.get("gateup_kernel", {})
+    line = {
+        "metric": METRIC,
+        "value": b1["us_per_layer"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(b1["us_per_layer"] / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (int8 weights, fp32 activations and accumulation)",
+        "data": "synthetic",
+        "config": {"workload": "int8 MoE decode layer, batch 1, 11 seeded layers rotated (cold HBM), HIP graph",
+                   "hidden": H, "moe_ffn": F, "routed_experts": E, "top_k": TOPK, "shared_ffn": FS,
+                   "group": GROUP, "batch": 1, "layers_rotated": LAYERS},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_gateup (routed int8 gate+up, shared gate+up, SwiGLU), decode B=1",
+            "achieved": gu.get("gbs"),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4) if gu else None,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": gu.get("avg_bytes"),
+            "avg_launch_us": gu.get("avg_us"),
+        },
+        "cpu_baseline": None if cpu is None else {
+            "value": cpu["b1_us"], "unit": "us", "cores": cpu["cores"], "kind": "port",
+            "sample": f"int8 decode layer B=1, median of {cpu['b1_runs']} runs (B=8: {cpu['b8_us']} us, "
+                      f"{cpu['b8_runs']} runs); the reference's CPU decomposition restated in C",
+        },
+        "results": results,
+        "wall_s": round(time.perf_counter() - t_start, 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -156,6 +156,19 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden,
 /* Frees the library's own workspaces (those used when workspace == NULL). */
 void uocr_moe_release(void);
 
+/* ---------------------------------------------------------------------------
+ * Kernel timing (no counterpart in the reference; for benchmarks).  After
+ * uocr_moe_timing_begin(capacity), each of the next `capacity` kernel
+ * launches of this library records a start/stop event pair around the kernel
+ * (hipExtLaunchKernelGGL).  uocr_moe_timing_end waits for them and writes, per
+ * launch in order, the duration in ms and the kernel's name (NUL-terminated,
+ * name_stride bytes apart); it ends the timing.  Not for use under stream
+ * capture; not thread-safe against concurrent callers.
+ * ------------------------------------------------------------------------- */
+int uocr_moe_timing_begin(int capacity, char* err, size_t errlen);
+int uocr_moe_timing_end(int capacity, float* ms, char* names, size_t name_stride, int* count,
+                        char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -277,7 +277,7 @@ hipError_t launch_dequant(void* out, int out_f32, const int8_t* w, const float* 
   const int64_t total = (int64_t)N * K;
   if (total == 0) return hipSuccess;
   const int64_t blocks = (total + 8 * 256 - 1) / (8 * 256);
-  hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, s, out, out_f32, w, scales, idx, E, N, K,
+  UOCR_LAUNCH("dequant", k_dequant, dim3((unsigned)blocks), dim3(256), 0, s, out, out_f32, w, scales, idx, E, N, K,
                      groups, vec);
   return hipGetLastError();
 }
@@ -296,14 +296,14 @@ hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared
   const dim3 grid(wgs), block(kGemmThreads);
   if (routed.kind == kInt8Rows) {
     if (nproj == 2)
-      hipLaunchKernelGGL((k_gemm_pair<kInt8Rows, 2, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemm_gateup", (k_gemm_pair<kInt8Rows, 2, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
     else
-      hipLaunchKernelGGL((k_gemm_pair<kInt8Rows, 1, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemm_down", (k_gemm_pair<kInt8Rows, 1, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
   } else {
     if (nproj == 2)
-      hipLaunchKernelGGL((k_gemm_pair<kBf16Rows, 2, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemm_gateup", (k_gemm_pair<kBf16Rows, 2, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
     else
-      hipLaunchKernelGGL((k_gemm_pair<kBf16Rows, 1, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemm_down", (k_gemm_pair<kBf16Rows, 1, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
   }
   return hipGetLastError();
 }

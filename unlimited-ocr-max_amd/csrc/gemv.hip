@@ -293,9 +293,9 @@ hipError_t launch_gemv(const GemvArgs& a, int max_groups, int nproj, int waves, 
   const dim3 grid(wgs), block(waves * kWave);
   if (nproj == 1) {
     switch (a.kind) {
-      case kInt8Rows: hipLaunchKernelGGL((k_gemv1<kInt8Rows, 1>), grid, block, lds, s, a); break;
-      case kBf16Rows: hipLaunchKernelGGL((k_gemv1<kBf16Rows, 1>), grid, block, lds, s, a); break;
-      case kBf16KBlocked: hipLaunchKernelGGL((k_gemv1<kBf16KBlocked, 1>), grid, block, lds, s, a); break;
+      case kInt8Rows: UOCR_LAUNCH("gemv_op", (k_gemv1<kInt8Rows, 1>), grid, block, lds, s, a); break;
+      case kBf16Rows: UOCR_LAUNCH("gemv_op", (k_gemv1<kBf16Rows, 1>), grid, block, lds, s, a); break;
+      case kBf16KBlocked: UOCR_LAUNCH("gemv_op", (k_gemv1<kBf16KBlocked, 1>), grid, block, lds, s, a); break;
     }
   } else {
     return hipErrorInvalidValue;  // the fused gate/up pair runs through launch_gemv_pair
@@ -311,14 +311,14 @@ hipError_t launch_gemv_pair(const GemvArgs& routed, int max_groups, const GemvAr
   const dim3 grid(wgs), block(waves * kWave);
   if (routed.kind == kInt8Rows) {
     if (nproj == 2)
-      hipLaunchKernelGGL((k_gemv2<kInt8Rows, 2, kBf16KBlocked, 2>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemv_gateup", (k_gemv2<kInt8Rows, 2, kBf16KBlocked, 2>), grid, block, lds, s, routed, shared, split);
     else
-      hipLaunchKernelGGL((k_gemv2<kInt8Rows, 1, kBf16KBlocked, 1>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemv_down", (k_gemv2<kInt8Rows, 1, kBf16KBlocked, 1>), grid, block, lds, s, routed, shared, split);
   } else {
     if (nproj == 2)
-      hipLaunchKernelGGL((k_gemv2<kBf16Rows, 2, kBf16KBlocked, 2>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemv_gateup", (k_gemv2<kBf16Rows, 2, kBf16KBlocked, 2>), grid, block, lds, s, routed, shared, split);
     else
-      hipLaunchKernelGGL((k_gemv2<kBf16Rows, 1, kBf16KBlocked, 1>), grid, block, lds, s, routed, shared, split);
+      UOCR_LAUNCH("gemv_down", (k_gemv2<kBf16Rows, 1, kBf16KBlocked, 1>), grid, block, lds, s, routed, shared, split);
   }
   return hipGetLastError();
 }

@@ -201,10 +201,10 @@ hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float
   if (T <= 8) {
     // decode: one wave per expert, every token of the step against it
     const dim3 grid((E + 3) / 4, 1);
-    hipLaunchKernelGGL((k_logits<8, 1>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
+    UOCR_LAUNCH("logits", (k_logits<8, 1>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
   } else {
     const dim3 grid((E + 15) / 16, (T + 15) / 16);
-    hipLaunchKernelGGL((k_logits<16, 4>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
+    UOCR_LAUNCH("logits", (k_logits<16, 4>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
   }
   return hipGetLastError();
 }
@@ -212,28 +212,28 @@ hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float
 hipError_t launch_softmax_topk(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
                                int64_t* ids64, float* wts, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_softmax_topk, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, topk, renorm, ids32, ids64,
+  UOCR_LAUNCH("softmax_topk", k_softmax_topk, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, topk, renorm, ids32, ids64,
                      wts);
   return hipGetLastError();
 }
 
 hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s) {
   if (E > kMaxGroupExperts) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, s, ids, R, E, bm, g);
+  UOCR_LAUNCH("group", k_group, dim3(1), dim3(1024), 0, s, ids, R, E, bm, g);
   return hipGetLastError();
 }
 
 hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
                               const GroupTables& g, hipStream_t s) {
   if (T > kSmallTokens || E > 64 || topk > 64) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_route_small, dim3(1), dim3(1024), 0, s, logits, T, E, topk, renorm, ids32, wts, g);
+  UOCR_LAUNCH("route_small", k_route_small, dim3(1), dim3(1024), 0, s, logits, T, E, topk, renorm, ids32, wts, g);
   return hipGetLastError();
 }
 
 hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* wts, const int32_t* inv,
                           const float* shared, int T, int H, int topk, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, T), dim3(256), 0, s, out, y, ldy, wts, inv, shared, T, H, topk);
+  UOCR_LAUNCH("combine", k_combine, dim3((H + 255) / 256, T), dim3(256), 0, s, out, y, ldy, wts, inv, shared, T, H, topk);
   return hipGetLastError();
 }
 

@@ -2,11 +2,26 @@
 // the kernel translation units.  Not part of the public header.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace uocr {
+
+// Kernel timing for benchmarks: while uocr_moe_timing_begin() is in effect,
+// timing_slot() hands out a start/stop event pair per launch (until the
+// capacity runs out) and the launch records them around the kernel.
+bool timing_slot(const char* name, hipEvent_t* start, hipEvent_t* stop);
+
+#define UOCR_LAUNCH(name, kernel, grid, block, shmem, stream, ...)                                   \
+  do {                                                                                               \
+    hipEvent_t uocr_t0_ = nullptr, uocr_t1_ = nullptr;                                               \
+    if (::uocr::timing_slot(name, &uocr_t0_, &uocr_t1_))                                             \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, uocr_t0_, uocr_t1_, 0, __VA_ARGS__); \
+    else                                                                                             \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                           \
+  } while (0)
 
 // Elements per chunk of the bf16 chains (the int8 chains use the quant group).
 constexpr int kChunk = 128;

@@ -10,7 +10,9 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <string>
 #include <utility>
+#include <vector>
 
 #include "uocr_kernels.h"
 
@@ -21,6 +23,31 @@ int gemm_bk();
 }  // namespace uocr
 
 using namespace uocr;
+
+// ------------------------------------------------------------------ kernel timing
+
+namespace {
+
+struct Timing {
+  std::mutex mu;
+  bool on = false;
+  size_t used = 0;
+  std::vector<hipEvent_t> start, stop;
+  std::vector<std::string> names;
+};
+Timing g_timing;
+
+}  // namespace
+
+bool uocr::timing_slot(const char* name, hipEvent_t* start, hipEvent_t* stop) {
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  if (!g_timing.on || g_timing.used >= g_timing.start.size()) return false;
+  *start = g_timing.start[g_timing.used];
+  *stop = g_timing.stop[g_timing.used];
+  g_timing.names[g_timing.used] = name;
+  ++g_timing.used;
+  return true;
+}
 
 namespace {
 
@@ -565,6 +592,43 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   if (e == hipSuccess && expert_weights)
     e = hipMemcpyAsync(expert_weights, d.wts, R * sizeof(float), hipMemcpyDeviceToDevice, s);
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+int uocr_moe_timing_begin(int capacity, char* err, size_t errlen) {
+  if (capacity < 1) return fail(err, errlen, "uocr_moe_timing_begin: capacity must be >= 1");
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  while ((int)g_timing.start.size() < capacity) {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e != hipSuccess) return hip_fail(err, errlen, "uocr_moe_timing_begin", e);
+    g_timing.start.push_back(a);
+    g_timing.stop.push_back(b);
+    g_timing.names.emplace_back();
+  }
+  g_timing.used = 0;
+  g_timing.on = true;
+  return 0;
+}
+
+int uocr_moe_timing_end(int capacity, float* ms, char* names, size_t name_stride, int* count, char* err,
+                        size_t errlen) {
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  g_timing.on = false;
+  const int n = (int)(g_timing.used < (size_t)capacity ? g_timing.used : (size_t)capacity);
+  for (int i = 0; i < n; ++i) {
+    hipError_t e = hipEventSynchronize(g_timing.stop[i]);
+    float t = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, g_timing.start[i], g_timing.stop[i]);
+    if (e != hipSuccess) return hip_fail(err, errlen, "uocr_moe_timing_end", e);
+    if (ms) ms[i] = t;
+    if (names && name_stride > 0) {
+      std::snprintf(names + (size_t)i * name_stride, name_stride, "%s", g_timing.names[i].c_str());
+    }
+  }
+  if (count) *count = n;
+  g_timing.used = 0;
+  return 0;
 }
 
 void uocr_moe_release(void) {

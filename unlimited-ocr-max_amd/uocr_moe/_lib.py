@@ -53,6 +53,8 @@ SIGNATURES: dict[str, list] = {
     "uocr_moe_decode_rows": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_forward": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_release": [],
+    "uocr_moe_timing_begin": [_int, _cp, _sz],
+    "uocr_moe_timing_end": [_int, _vp, _vp, _sz, ctypes.POINTER(_int), _cp, _sz],
 }
 _RESTYPES = {"uocr_moe_workspace_bytes": _sz, "uocr_moe_release": None}
 
@@ -83,3 +85,20 @@ def call(name: str, *args) -> None:
     rc = getattr(load(), name)(*args, err, ERRLEN)
     if rc != 0:
         raise UocrError(err.value.decode() or f"{name} failed with code {rc}")
+
+
+def timing_begin(capacity: int) -> None:
+    """Records a start/stop event pair around each of the next ``capacity`` kernel launches."""
+    call("uocr_moe_timing_begin", int(capacity))
+
+
+def timing_end(capacity: int) -> list[tuple[str, float]]:
+    """``[(kernel name, ms)]`` of the launches recorded since :func:`timing_begin`, in order."""
+    import numpy as np
+
+    ms = np.zeros(capacity, np.float32)
+    names = ctypes.create_string_buffer(capacity * 32)
+    count = _int(0)
+    call("uocr_moe_timing_end", int(capacity), ms.ctypes.data, ctypes.addressof(names), 32, ctypes.byref(count))
+    raw = names.raw
+    return [(raw[i * 32 : (i + 1) * 32].split(b"\0", 1)[0].decode(), float(ms[i])) for i in range(count.value)]

@@ -57,7 +57,9 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _rows_per_read(rows: int, out_dim: int) -> int:
-    """The reference's tile rule for dense_bf16_qmv (unlimited_ocr_max/decoder.py:144-163)."""
+    """The reference's tile rule for dense_bf16_qmv (unlimited_ocr_max/decoder.py:144-163); 1 for no rows."""
+    if rows <= 0:
+        return 1
     tiles = 1
     while True:
         tile = math.ceil(rows / tiles)
