@@ -153,8 +153,14 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden,
                      const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
                      void* workspace, size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
-/* Frees the library's own workspaces (those used when workspace == NULL). */
+/* Frees the library's own workspaces (those used when workspace == NULL) and
+ * control words.  No call may be in flight. */
 void uocr_moe_release(void);
+
+/* Waits for `stream` and reports whether any persistent decode launch on it
+ * ran out of its bounded waits (errors = 1: those launches' outputs are wrong).
+ * No counterpart in the reference; a diagnostic of this build's decode kernel. */
+int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen);
 
 /* ---------------------------------------------------------------------------
  * Kernel timing (no counterpart in the reference; for benchmarks).  After

@@ -72,26 +72,40 @@ def test_gate_ties_and_renorm(oracle) -> None:
 # ----------------------------------------------------------------------------- decode
 
 
+@pytest.fixture(params=["fused", "multi"])
+def decode_path(request, monkeypatch):
+    """The persistent one-kernel decode (B <= 8) and the multi-kernel decode: same bits."""
+    if request.param == "multi":
+        monkeypatch.setenv("UOCR_MOE_DECODE", "multi")
+    else:
+        monkeypatch.delenv("UOCR_MOE_DECODE", raising=False)
+    yield request.param
+    if request.param == "fused":
+        from uocr_moe import _lib
+
+        assert _lib.fused_errors() == 0
+
+
 @pytest.mark.parametrize("int8", [True, False], ids=["int8", "bf16"])
-def test_decode_small_layer_bitwise(oracle, small, int8) -> None:
+def test_decode_small_layer_bitwise(oracle, small, int8, decode_path) -> None:
     layer = small[int8]
     moe = moe_for(layer)
     x = np.random.default_rng(23).standard_normal((8, 256)).astype(np.float32)
     out, ids, wts = moe.decode_rows(t(x), routing=True)
     want, ids_o, wts_o = oracle.moe_decode_exact(x, layer)
-    print(f"[uocr] decode small {'int8' if int8 else 'bf16'}: {differ(n(out), want)} differ")
+    print(f"[uocr] decode small {'int8' if int8 else 'bf16'} {decode_path}: {differ(n(out), want)} differ")
     assert np.array_equal(n(ids), ids_o) and bits_equal(n(wts), wts_o)
     assert bits_equal(n(out), want)
 
 
-@pytest.mark.parametrize("B", [1, 8])
-def test_decode_full_int8_bitwise(oracle, full_int8, B) -> None:
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_decode_full_int8_bitwise(oracle, full_int8, B, decode_path) -> None:
     moe = moe_for(full_int8)
     x = oracle.rmsnorm_rows(np.random.default_rng(100 + B), B, 1280)
     out, ids, wts = moe.decode_rows(t(x), routing=True)
     got = n(out)
     want, ids_o, wts_o = oracle.moe_decode_exact(x, full_int8)
-    print(f"[uocr] decode int8 B={B}: {differ(got, want)} of {got.size} differ")
+    print(f"[uocr] decode int8 B={B} {decode_path}: {differ(got, want)} of {got.size} differ")
     assert np.array_equal(n(ids), ids_o)
     assert bits_equal(got, want)
     exact = oracle.moe_layer_f64(x, full_int8, ids_o, wts_o)
@@ -103,7 +117,7 @@ def test_decode_full_int8_bitwise(oracle, full_int8, B) -> None:
 
 
 @pytest.mark.parametrize("B", [1, 8])
-def test_decode_full_bf16_bitwise(oracle, full_bf16, B) -> None:
+def test_decode_full_bf16_bitwise(oracle, full_bf16, B, decode_path) -> None:
     moe = moe_for(full_bf16)
     x = oracle.rmsnorm_rows(np.random.default_rng(200 + B), B, 1280)
     got = n(moe.decode_rows(t(x)))
@@ -111,6 +125,31 @@ def test_decode_full_bf16_bitwise(oracle, full_bf16, B) -> None:
     assert bits_equal(got, want)
     exact = oracle.moe_layer_f64(x, full_bf16, ids_o, wts_o)
     assert oracle.rel_err(got, exact) <= 1e-4
+
+
+def test_decode_repeated_calls_and_graph_replays(oracle, small) -> None:
+    """The persistent kernel leaves its control words clean: back-to-back launches, eager and
+    captured in a HIP graph replayed several times with eager work between replays, all bitwise."""
+    layer = small[True]
+    moe = moe_for(layer)
+    xs = [np.random.default_rng(60 + i).standard_normal((1 + i % 8, 256)).astype(np.float32) for i in range(12)]
+    want = [oracle.moe_decode_exact(x, layer)[0] for x in xs]
+    for x, w in zip(xs, want):
+        assert bits_equal(n(moe.decode_rows(t(x))), w)
+    xg = t(xs[3])
+    ws = moe.workspace(xg.shape[0], prefill=False)
+    moe.decode_rows(xg, workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outg = moe.decode_rows(xg, workspace=ws)
+    for _ in range(4):
+        graph.replay()
+        assert bits_equal(n(outg), want[3])
+        assert bits_equal(n(moe.decode_rows(t(xs[5]))), want[5])
+    from uocr_moe import _lib
+
+    assert _lib.fused_errors() == 0
 
 
 def test_decode_batch_of_64_and_workspace(oracle, small) -> None:

@@ -19,7 +19,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "uocr_moe" / "libuocr_moe.so"
-SOURCES = ["gemv.hip", "route.hip", "gemm.hip", "uocr_moe.cpp"]
+SOURCES = ["gemv.hip", "route.hip", "gemm.hip", "decode.hip", "uocr_moe.cpp"]
 ARCH = os.environ.get("UOCR_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -43,9 +43,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP library needs ROCm's hipcc")
 
 
-def _compile(src: str) -> Path:
-    obj = BUILD / (src + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(src: str, build_dir: Path = BUILD, defines: tuple[str, ...] = ()) -> Path:
+    obj = build_dir / (src + ".o")
+    cmd = [hipcc(), *FLAGS, *[f"-D{d}" for d in defines], "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
         cmd.insert(1, "-x")
         cmd.insert(2, "hip")
@@ -55,20 +55,24 @@ def _compile(src: str) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source (always) and link the shared library; returns its path."""
-    BUILD.mkdir(exist_ok=True)
+def build(verbose: bool = False, lib: Path = LIB, build_dir: Path = BUILD, defines: tuple[str, ...] = ()) -> Path:
+    """Compile every source (always) and link the shared library; returns its path.
+
+    ``defines`` (``NAME=VALUE``) and a separate ``lib``/``build_dir`` build variants for experiments.
+    """
+    build_dir.mkdir(parents=True, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as pool:
-        objs = list(pool.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(pool.map(lambda s: _compile(s, build_dir, defines), SOURCES))
+    LIB_ = lib
+    tmp = LIB_.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, LIB_)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {LIB_}")
+    return LIB_
 
 
 if __name__ == "__main__":

@@ -28,12 +28,22 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // are read once per call, so they should not evict activations and tables.
 // (Pointers reach the kernels inside argument structs, where the compiler
 // sees generic pointers; the casts state the global address space.)
+#ifndef UOCR_WEIGHT_NT
+#define UOCR_WEIGHT_NT 1
+#endif
+__device__ __forceinline__ i32x4 load_w16(const void* p) {
+#if UOCR_WEIGHT_NT
+  return __builtin_nontemporal_load((const UOCR_GLOBAL i32x4*)p);
+#else
+  return *(const UOCR_GLOBAL i32x4*)p;
+#endif
+}
 __device__ __forceinline__ int4 load_nt16(const void* p) {
-  const i32x4 v = __builtin_nontemporal_load((const UOCR_GLOBAL i32x4*)p);
+  const i32x4 v = load_w16(p);
   return make_int4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ uint4 load_nt16u(const void* p) {
-  const i32x4 v = __builtin_nontemporal_load((const UOCR_GLOBAL i32x4*)p);
+  const i32x4 v = load_w16(p);
   return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
 

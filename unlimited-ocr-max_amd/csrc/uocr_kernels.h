@@ -135,4 +135,54 @@ struct GemmProblem {
 hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles,
                             hipStream_t s);
 
+// ---- the persistent decode layer (decode.hip) ----
+
+struct FusedArgs {
+  int B, E, H, F, Fs, topk;
+  int int8, renorm;
+  const float* router;
+  const void* gate_w;
+  const void* up_w;
+  const void* down_w;
+  const float* gate_s;
+  const float* up_s;
+  const float* down_s;
+  const uint16_t* sh_gate;
+  const uint16_t* sh_up;
+  const uint16_t* sh_down;
+  const float* x;
+  float* out;
+  // control words (library-owned, zero between launches)
+  uint32_t* ctl;
+  int ctl_words;
+  // workspace
+  float* logits;  // [B][64]
+  int* ids;       // [B*topk]
+  float* wts;     // [B*topk]
+  int* n_groups;
+  int* group_expert;  // [64]
+  int* group_start;   // [65]
+  int* group_rows;    // [64]
+  float* p_sgu;
+  float* p_rgu;
+  float* s_rgu;
+  float* p_sdn;
+  float* p_rdn;
+  float* s_rdn;
+  float* hs;  // [B][Fs]
+  float* h;   // [B*topk][F]
+  float* sh;  // [B][H]
+  float* y;   // [B*topk][H]
+  // task layout
+  int cb_f, cb_fs, cb_h;  // 64-column blocks of F, Fs, H
+  int ch_h, ch_f, ch_fs;  // 128-element chunks of H, F, Fs
+  int max_slots;
+  int n_router, n_sgu, n_rgu, n_sdn, n_rdn, n_tasks;
+};
+int fused_ctl_words(int cb_fs, int cb_h, int cb_f, int max_slots);
+size_t fused_lds_bytes(int B);
+hipError_t fused_grid(int B, int* grid);
+hipError_t launch_decode_fused(const FusedArgs& a, int grid, hipStream_t s);
+hipError_t launch_zero_words(uint32_t* p, int n, hipStream_t s);
+
 }  // namespace uocr

@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -112,6 +113,47 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
   }
   *out = b.ptr;
   return hipSuccess;
+}
+
+// Control words of the persistent decode kernel, per (device, stream): zeroed
+// once when created; every launch leaves them zero again.
+constexpr int kCtlWords = 1 << 14;
+std::map<std::pair<int, hipStream_t>, uint32_t*> g_ctl;
+
+hipError_t ctl_words(hipStream_t stream, uint32_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  uint32_t*& p = g_ctl[{dev, stream}];
+  if (p == nullptr) {
+    e = hipMalloc(&p, kCtlWords * sizeof(uint32_t));
+    if (e != hipSuccess) {
+      p = nullptr;
+      return e;
+    }
+    e = launch_zero_words(p, kCtlWords, stream);
+    if (e != hipSuccess) return e;
+  }
+  *out = p;
+  return hipSuccess;
+}
+
+std::map<std::pair<int, int>, int> g_fused_grid;  // (device, B) -> workgroups
+
+hipError_t fused_grid_cached(int B, int* grid) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  auto it = g_fused_grid.find({dev, B});
+  if (it != g_fused_grid.end()) {
+    *grid = it->second;
+    return hipSuccess;
+  }
+  e = fused_grid(B, grid);
+  if (e == hipSuccess) g_fused_grid[{dev, B}] = *grid;
+  return e;
 }
 
 // Resolves the workspace of a call: the caller's (checked for size) or ours.
@@ -328,6 +370,60 @@ static DecodeBufs carve_decode(Carve& c, const uocr_moe_layer* L, int64_t B) {
   return d;
 }
 
+static bool fused_eligible(const uocr_moe_layer* L, int64_t B) {
+  const char* env = std::getenv("UOCR_MOE_DECODE");
+  if (env != nullptr && std::strcmp(env, "multi") == 0) return false;
+  if (B < 1 || B > 8 || B * L->top_k > 64 || L->num_experts > 64) return false;
+  if (L->hidden % 128 || L->ffn % 128 || L->shared_ffn % 128) return false;
+  if (L->int8 && L->group != 128) return false;
+  return true;
+}
+
+static FusedArgs carve_fused(Carve& c, const uocr_moe_layer* L, int64_t B) {
+  FusedArgs a{};
+  const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
+  const int topk = (int)L->top_k;
+  const int R = (int)B * topk;
+  a.B = (int)B;
+  a.E = E;
+  a.H = H;
+  a.F = F;
+  a.Fs = Fs;
+  a.topk = topk;
+  a.cb_f = F / 64;
+  a.cb_fs = Fs / 64;
+  a.cb_h = H / 64;
+  a.ch_h = H / 128;
+  a.ch_f = F / 128;
+  a.ch_fs = Fs / 128;
+  a.max_slots = E < R ? E : R;
+  a.n_router = E;
+  a.n_sgu = a.cb_fs * 2 * a.ch_h;
+  a.n_rgu = a.max_slots * a.cb_f * 2 * a.ch_h;
+  a.n_sdn = a.cb_h * a.ch_fs;
+  a.n_rdn = a.max_slots * a.cb_h * a.ch_f;
+  a.n_tasks = a.n_router + a.n_sgu + a.n_rgu + a.n_sdn + a.n_rdn;
+  a.ctl_words = fused_ctl_words(a.cb_fs, a.cb_h, a.cb_f, a.max_slots);
+  a.logits = c.take<float>(B * 64);
+  a.ids = c.take<int>(R);
+  a.wts = c.take<float>(R);
+  a.n_groups = c.take<int>(1);
+  a.group_expert = c.take<int>(64);
+  a.group_start = c.take<int>(65);
+  a.group_rows = c.take<int>(64);
+  a.p_sgu = c.take<float>((size_t)a.cb_fs * 2 * a.ch_h * B * 64);
+  a.p_rgu = c.take<float>((size_t)a.max_slots * a.cb_f * 2 * a.ch_h * B * 64);
+  a.s_rgu = c.take<float>((size_t)a.max_slots * a.cb_f * 2 * a.ch_h * 64);
+  a.p_sdn = c.take<float>((size_t)a.cb_h * a.ch_fs * B * 64);
+  a.p_rdn = c.take<float>((size_t)a.max_slots * a.cb_h * a.ch_f * B * 64);
+  a.s_rdn = c.take<float>((size_t)a.max_slots * a.cb_h * a.ch_f * 64);
+  a.hs = c.take<float>(B * Fs);
+  a.h = c.take<float>((size_t)R * F);
+  a.sh = c.take<float>(B * H);
+  a.y = c.take<float>((size_t)R * H);
+  return a;
+}
+
 struct PrefillBufs {
   float* logits;
   int32_t* ids;
@@ -356,10 +452,16 @@ static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
 size_t uocr_moe_workspace_bytes(const uocr_moe_layer* layer, int64_t rows, int prefill) {
   if (layer == nullptr || rows < 0) return 0;
   Carve c(nullptr);
-  if (prefill)
+  if (prefill) {
     carve_prefill(c, layer, rows);
-  else
+  } else {
     carve_decode(c, layer, rows);
+    if (fused_eligible(layer, rows)) {
+      Carve f(nullptr);
+      carve_fused(f, layer, rows);
+      if (f.off > c.off) c.off = f.off;
+    }
+  }
   return c.off + 256;
 }
 
@@ -393,6 +495,39 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
   if (rows == 0) return 0;
   const hipStream_t s = (hipStream_t)stream;
   const int64_t B = rows, R = rows * L->top_k;
+  if (fused_eligible(L, B)) {
+    Carve dry(nullptr);
+    carve_fused(dry, L, B);
+    void* ws = nullptr;
+    if (resolve_workspace(op, workspace, workspace_bytes, dry.off, s, &ws, err, errlen)) return 1;
+    Carve c(ws);
+    FusedArgs a = carve_fused(c, L, B);
+    if (a.ctl_words > kCtlWords) return fail(err, errlen, "%s: the layer needs too many control words", op);
+    hipError_t e = ctl_words(s, &a.ctl);
+    int grid = 0;
+    if (e == hipSuccess) e = fused_grid_cached((int)B, &grid);
+    if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+    a.int8 = L->int8;
+    a.renorm = L->renormalize;
+    a.router = L->router;
+    a.gate_w = L->gate_proj;
+    a.up_w = L->up_proj;
+    a.down_w = L->down_proj;
+    a.gate_s = L->gate_proj_scales;
+    a.up_s = L->up_proj_scales;
+    a.down_s = L->down_proj_scales;
+    a.sh_gate = L->shared_gate;
+    a.sh_up = L->shared_up;
+    a.sh_down = L->shared_down;
+    a.x = x;
+    a.out = out;
+    e = launch_decode_fused(a, grid, s);
+    if (e == hipSuccess && expert_ids)
+      e = hipMemcpyAsync(expert_ids, a.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess && expert_weights)
+      e = hipMemcpyAsync(expert_weights, a.wts, R * sizeof(float), hipMemcpyDeviceToDevice, s);
+    return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+  }
   Carve dry(nullptr);
   carve_decode(dry, L, B);
   void* ws = nullptr;
@@ -631,11 +766,25 @@ int uocr_moe_timing_end(int capacity, float* ms, char* names, size_t name_stride
   return 0;
 }
 
+int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen) {
+  uint32_t* ctl = nullptr;
+  hipError_t e = ctl_words((hipStream_t)stream, &ctl);
+  uint32_t v = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&v, ctl + 4, sizeof(v), hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(err, errlen, "uocr_moe_fused_errors", e);
+  if (errors) *errors = v;
+  return 0;
+}
+
 void uocr_moe_release(void) {
   std::lock_guard<std::mutex> lock(g_ws_mu);
   for (auto& kv : g_ws)
     if (kv.second.ptr != nullptr) (void)hipFree(kv.second.ptr);
   g_ws.clear();
+  for (auto& kv : g_ctl)
+    if (kv.second != nullptr) (void)hipFree(kv.second);
+  g_ctl.clear();
 }
 
 }  // extern "C"

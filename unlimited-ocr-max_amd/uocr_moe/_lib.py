@@ -54,6 +54,7 @@ SIGNATURES: dict[str, list] = {
     "uocr_moe_forward": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_release": [],
     "uocr_moe_timing_begin": [_int, _cp, _sz],
+    "uocr_moe_fused_errors": [_vp, ctypes.POINTER(ctypes.c_uint32), _cp, _sz],
     "uocr_moe_timing_end": [_int, _vp, _vp, _sz, ctypes.POINTER(_int), _cp, _sz],
 }
 _RESTYPES = {"uocr_moe_workspace_bytes": _sz, "uocr_moe_release": None}
@@ -102,3 +103,14 @@ def timing_end(capacity: int) -> list[tuple[str, float]]:
     call("uocr_moe_timing_end", int(capacity), ms.ctypes.data, ctypes.addressof(names), 32, ctypes.byref(count))
     raw = names.raw
     return [(raw[i * 32 : (i + 1) * 32].split(b"\0", 1)[0].decode(), float(ms[i])) for i in range(count.value)]
+
+
+def fused_errors(stream: int | None = None) -> int:
+    """Synchronises ``stream`` (default: torch's current) and returns the persistent decode kernel's error word."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    v = ctypes.c_uint32(0)
+    call("uocr_moe_fused_errors", stream, ctypes.byref(v))
+    return int(v.value)
