@@ -162,6 +162,15 @@ void uocr_moe_release(void);
  * No counterpart in the reference; a diagnostic of this build's decode kernel. */
 int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen);
 
+/* Arms a phase trace for the next persistent decode launch: for task i it
+ * writes 8 int64 words at buffer[8i] (device memory, `words` long):
+ * wall-clock stamps of its phases (0 start, 1 routing known, 2 weights
+ * arrived, 3 activations ready, 4 chain done, 5 counter updated, 6 end) and
+ * word 7 the wave that ran it.  grid_waves receives the waves of the last
+ * launch configuration.  A diagnostic of this build's decode kernel; tracing
+ * waits for each task's loads, so a traced launch runs slower. */
+int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err, size_t errlen);
+
 /* ---------------------------------------------------------------------------
  * Kernel timing (no counterpart in the reference; for benchmarks).  After
  * uocr_moe_timing_begin(capacity), each of the next `capacity` kernel

@@ -101,6 +101,12 @@ __device__ __forceinline__ const float* uniform_ptr(const float* p) {
 // holds that many rows so padded rows read inside it.
 __host__ __device__ constexpr int padded_rows(int B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
 
+// Phase timestamps of a task (the constant-rate wall clock), when tracing.
+#define UOCR_TRACE(a, task, slot)                                                    \
+  do {                                                                               \
+    if ((a).trace != nullptr && lane_id() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
+  } while (0)
+
 enum TaskKind : int { T_ROUTER = 0, T_SGU = 1, T_RGU = 2, T_SDN = 3, T_RDN = 4, T_NONE = 5 };
 
 struct Task {
@@ -225,8 +231,8 @@ struct XSrc {
 
 // Elements of the chunk handled per step: 16, or 8 for 8 rows (the x values
 // of a step live in scalar registers).
-template <int R>
-constexpr int kStep = R > 4 ? 8 : 16;
+template <int R, bool LDSX>
+constexpr int kStep = LDSX ? 4 : (R > 4 ? 8 : 16);
 
 // x[r][k..k+S-1] of every row r < R into registers: scalar loads of the kernel
 // input, or LDS broadcasts of a staged activation.
@@ -254,7 +260,7 @@ __device__ __forceinline__ void load_x(const XSrc& xs, int k, float (&xv)[8][16]
 // into part[] in k order.
 template <int R, bool LDSX>
 __device__ __forceinline__ void chain_int8(const char* tile, const XSrc& xs, float (&part)[8]) {
-  constexpr int S = kStep<R>;
+  constexpr int S = kStep<R, LDSX>;
   const int l = lane_id();
 #pragma unroll 1
   for (int k0 = 0; k0 < 128; k0 += S) {
@@ -274,22 +280,24 @@ __device__ __forceinline__ void chain_int8(const char* tile, const XSrc& xs, flo
 // One bf16 sub-tile: the lane's 64 weights of its row (k = koff..koff+63).
 template <int R, bool LDSX>
 __device__ __forceinline__ void chain_bf16(const char* tile, const XSrc& xs, int koff, float (&part)[8]) {
-  constexpr int S = kStep<R>;
+  constexpr int S = kStep<R, LDSX>;
   const int l = lane_id();
 #pragma unroll 1
   for (int k0 = 0; k0 < 64; k0 += S) {
     float xv[8][16];
     load_x<R, S, LDSX>(xs, koff + k0, xv);
+    // 16-byte pieces of 8 bf16 covering the step
+    constexpr int NP = S >= 8 ? S / 8 : 1;
+    i32x4 wq[NP];
 #pragma unroll
-    for (int h8 = 0; h8 < S / 8; ++h8) {
-      const i32x4 wq = *(const i32x4*)(tile + l * kTileRow + (k0 + 8 * h8) * 2);
+    for (int pc = 0; pc < NP; ++pc) wq[pc] = *(const i32x4*)(tile + l * kTileRow + ((k0 & ~7) + 8 * pc) * 2);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t word = (uint32_t)wq[j >> 1];
-        const float wv = (j & 1) == 0 ? bf16_lo(word) : bf16_hi(word);
+    for (int j = 0; j < S; ++j) {
+      const int kk = (k0 & 7) + j;  // element counted from the first piece
+      const uint32_t word = (uint32_t)wq[kk >> 3][(kk & 7) >> 1];
+      const float wv = (kk & 1) == 0 ? bf16_lo(word) : bf16_hi(word);
 #pragma unroll
-        for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf(wv, xv[r][8 * h8 + j], part[r]);
-      }
+      for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf(wv, xv[r][j], part[r]);
     }
   }
 }
@@ -372,14 +380,26 @@ __device__ __attribute__((always_inline)) bool issue_task(const FusedArgs& a, co
   return false;
 }
 
-// router task: logits[t][e] for every token t of the step.
+// router task: logits[t][e] for every token t of the step (H <= 2048): the
+// lane's router values and each token's x values are loaded in one batch.
+constexpr int kMaxHPerLane = 32;
+
 __device__ __attribute__((always_inline)) void router_task(const FusedArgs& a, int e) {
   const int l = lane_id();
   const float* wr = a.router + (int64_t)e * a.H;
+  const int nk = (a.H - l + kWave - 1) / kWave;  // k = l + 64j, j < nk
+  float w[kMaxHPerLane];
+#pragma unroll
+  for (int j = 0; j < kMaxHPerLane; ++j) w[j] = j < nk ? ldg(wr + l + kWave * j) : 0.0f;
   for (int t = 0; t < a.B; ++t) {
-    const float* xr = a.x + (int64_t)t * a.H;
+    const float* xr = a.x + (int64_t)t * a.H + l;
+    float xv[kMaxHPerLane];
+#pragma unroll
+    for (int j = 0; j < kMaxHPerLane; ++j) xv[j] = j < nk ? ldg(xr + kWave * j) : 0.0f;
     float p = 0.0f;
-    for (int k = l; k < a.H; k += kWave) p = __builtin_fmaf(ldg(xr + k), ldg(wr + k), p);
+#pragma unroll
+    for (int j = 0; j < kMaxHPerLane; ++j)
+      if (j < nk) p = __builtin_fmaf(xv[j], w[j], p);
     const float v = wave_tree_sum(p);
     if (l == 0) st_dev(a.logits + t * 64 + e, v);
   }
@@ -465,31 +485,51 @@ __device__ __attribute__((always_inline)) Rows8 unit_rows(const FusedArgs& a, co
   return r;
 }
 
-// Stages activation rows (produced in this kernel) for a chunk: rows src[row*ld + k0 .. +128).
-__device__ __attribute__((always_inline)) void stage_rows(float* xstage, const float* src, int64_t ld, int64_t k0, const Rows8& rows) {
+// Stages activation rows (produced in this kernel) for a chunk: rows
+// src[row*ld + k0 .. +128), every load issued before the first LDS write.
+__device__ __attribute__((always_inline)) void stage_rows(float* xstage, const float* src, int64_t ld, int64_t k0,
+                                                         const Rows8& rows) {
   const int l = lane_id();
+  float v[16];
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
-    if (r >= rows.cnt) break;
     const float* srow = src + (int64_t)rows.row[r] * ld + k0;
-    xstage[r * 128 + l] = ld_dev(srow + l);
-    xstage[r * 128 + 64 + l] = ld_dev(srow + 64 + l);
+    v[2 * r] = r < rows.cnt ? ld_dev(srow + l) : 0.0f;
+    v[2 * r + 1] = r < rows.cnt ? ld_dev(srow + 64 + l) : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    if (r < rows.cnt) {
+      xstage[r * 128 + l] = v[2 * r];
+      xstage[r * 128 + 64 + l] = v[2 * r + 1];
+    }
   }
   __builtin_amdgcn_wave_barrier();
 }
 
-// Folds the partials of a unit in chunk order; returns acc[r] for the lane's column.
-__device__ __attribute__((always_inline)) void fold(const float* part, const float* scl, int chunks, int rm, int cnt, bool int8, float (&acc)[8]) {
+// Folds the partials of a unit in chunk order; returns acc[r] for the lane's
+// column.  Per row, the chunk partials (and the scales, once) are loaded in
+// one batch, then chained.
+constexpr int kMaxChunks = 16;
+
+__device__ __attribute__((always_inline)) void fold(const float* part, const float* scl, int chunks, int rm, int cnt,
+                                                   bool int8, float (&acc)[8]) {
   const int l = lane_id();
+  float s[kMaxChunks];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
-  for (int c = 0; c < chunks; ++c) {
-    const float s = int8 ? ld_dev(scl + c * 64 + l) : 1.0f;
+  for (int c = 0; c < kMaxChunks; ++c) s[c] = (int8 && c < chunks) ? ld_dev(scl + c * 64 + l) : 1.0f;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      if (r >= cnt) break;
-      const float v = ld_dev(part + (c * rm + r) * 64 + l);
-      acc[r] = int8 ? __builtin_fmaf(s, v, acc[r]) : acc[r] + v;
+  for (int r = 0; r < 8; ++r) {
+    acc[r] = 0.0f;
+    if (r < cnt) {
+      float v[kMaxChunks];
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) v[c] = c < chunks ? ld_dev(part + (c * rm + r) * 64 + l) : 0.0f;
+      float x = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c)
+        if (c < chunks) x = int8 ? __builtin_fmaf(s[c], v[c], x) : x + v[c];
+      acc[r] = x;
     }
   }
 }
@@ -498,13 +538,21 @@ __device__ __attribute__((always_inline)) void combine_block(const FusedArgs& a,
   const int l = lane_id();
   const int n = cb * 64 + l;
   if (n >= a.H) return;
+  constexpr int kMaxK = 8;
   for (int t = 0; t < a.B; ++t) {
-    float acc = 0.0f;
-    for (int j = 0; j < a.topk; ++j) {
+    float w[kMaxK], y[kMaxK];
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j) {
       const int i = t * a.topk + j;
-      acc = __builtin_fmaf(ld_dev(a.wts + i), ld_dev(a.y + (int64_t)i * a.H + n), acc);
+      w[j] = j < a.topk ? ld_dev(a.wts + i) : 0.0f;
+      y[j] = j < a.topk ? ld_dev(a.y + (int64_t)i * a.H + n) : 0.0f;
     }
-    a.out[(int64_t)t * a.H + n] = acc + ld_dev(a.sh + (int64_t)t * a.H + n);
+    const float shv = ld_dev(a.sh + (int64_t)t * a.H + n);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxK; ++j)
+      if (j < a.topk) acc = __builtin_fmaf(w[j], y[j], acc);
+    a.out[(int64_t)t * a.H + n] = acc + shv;
   }
 }
 
@@ -513,14 +561,20 @@ __device__ __attribute__((always_inline)) void after_down_fold(const FusedArgs& 
   if (signal(ctl_out(a) + cb) + 1u == target) combine_block(a, cb);
 }
 
-__device__ __attribute__((always_inline)) void chunk_task(const FusedArgs& a, const Wave& W, const Task& k) {
+__device__ __attribute__((always_inline)) void chunk_task(const FusedArgs& a, const Wave& W, const Task& k, int tid) {
   const int l = lane_id();
+  UOCR_TRACE(a, tid, 0);
   if (k.kind == T_RGU || k.kind == T_RDN) {
     wait_ge(a.ctl, C_READY, 1u);
     if (k.slot >= ld_dev(a.n_groups)) return;
   }
+  UOCR_TRACE(a, tid, 1);
   Stage st;
   issue_task(a, k, st);
+  if (a.trace != nullptr) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    UOCR_TRACE(a, tid, 2);
+  }
   const Rows8 rows = unit_rows(a, k);
   const bool routed = k.kind == T_RGU || k.kind == T_RDN;
   const bool int8 = routed && a.int8;
@@ -548,6 +602,7 @@ __device__ __attribute__((always_inline)) void chunk_task(const FusedArgs& a, co
     xs.from_lds = true;
   }
 
+  UOCR_TRACE(a, tid, 3);
   float part[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) part[r] = 0.0f;
@@ -597,7 +652,10 @@ __device__ __attribute__((always_inline)) void chunk_task(const FusedArgs& a, co
     const int groups = k.kind == T_RGU ? a.ch_h : a.ch_f;
     st_dev(sbase + pc * 64 + l, ldg(scales + ((int64_t)e * N + n) * groups + k.c));
   }
-  if (signal(counter) + 1u != (uint32_t)unit_chunks) return;
+  UOCR_TRACE(a, tid, 4);
+  const bool last = signal(counter) + 1u == (uint32_t)unit_chunks;
+  UOCR_TRACE(a, tid, 5);
+  if (!last) return;
 
   // ---- the last chunk of the unit: fold
   const bool valid = k.cb * 64 + l < N;
@@ -628,6 +686,7 @@ __device__ __attribute__((always_inline)) void chunk_task(const FusedArgs& a, co
     }
     after_down_fold(a, k.cb);
   }
+  UOCR_TRACE(a, tid, 6);
 }
 
 __global__ void __launch_bounds__(kWavesPerWg * 64) k_decode_fused(FusedArgs a) {
@@ -642,14 +701,19 @@ __global__ void __launch_bounds__(kWavesPerWg * 64) k_decode_fused(FusedArgs a) 
   for (; t < a.n_tasks; t += nwaves) {
     const Task k = decode_task(a, t);
     if (k.kind == T_ROUTER) {
+      UOCR_TRACE(a, t, 0);
       router_task(a, k.e);
+      UOCR_TRACE(a, t, 3);
       if (signal(a.ctl + C_ROUTER) + 1u == (uint32_t)a.n_router) {
+        UOCR_TRACE(a, t, 5);
         routing(a);
         signal(a.ctl + C_READY);
+        UOCR_TRACE(a, t, 6);
       }
     } else if (k.kind != T_NONE) {
-      chunk_task(a, W, k);
+      chunk_task(a, W, k, t);
     }
+    if (a.trace != nullptr && lane_id() == 0) a.trace[(int64_t)t * 8 + 7] = (int64_t)((int)blockIdx.x * kWavesPerWg + wv);
   }
 
   // the last wave of the launch resets the control words for the next one

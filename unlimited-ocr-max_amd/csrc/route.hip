@@ -38,16 +38,26 @@ __global__ void __launch_bounds__(256) k_logits(float* __restrict__ logits, cons
   for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int e = 0; e < EE; ++e) p[t][e] = 0.0f;
-  for (int k = lane; k < H; k += kWave) {
-    float xv[TT], wv[EE];
+  // k = lane + 64 j; U steps of loads are issued before their fmas
+  constexpr int U = TT * EE > 16 ? 2 : 4;
+  for (int k0 = lane; k0 < H; k0 += U * kWave) {
+    float xv[U][TT], wv[U][EE];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) xv[t] = xr[t][k];
+    for (int u = 0; u < U; ++u) {
+      const int k = k0 + u * kWave;
 #pragma unroll
-    for (int e = 0; e < EE; ++e) wv[e] = wr[e][k];
+      for (int t = 0; t < TT; ++t) xv[u][t] = k < H ? xr[t][k] : 0.0f;
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
+      for (int e = 0; e < EE; ++e) wv[u][e] = k < H ? wr[e][k] : 0.0f;
+    }
 #pragma unroll
-      for (int e = 0; e < EE; ++e) p[t][e] = __builtin_fmaf(xv[t], wv[e], p[t][e]);
+    for (int u = 0; u < U; ++u) {
+      if (k0 + u * kWave >= H) break;
+#pragma unroll
+      for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int e = 0; e < EE; ++e) p[t][e] = __builtin_fmaf(xv[u][t], wv[u][e], p[t][e]);
+    }
   }
 #pragma unroll
   for (int t = 0; t < TT; ++t)

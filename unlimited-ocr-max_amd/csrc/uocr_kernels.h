@@ -178,6 +178,8 @@ struct FusedArgs {
   int ch_h, ch_f, ch_fs;  // 128-element chunks of H, F, Fs
   int max_slots;
   int n_router, n_sgu, n_rgu, n_sdn, n_rdn, n_tasks;
+  // optional per-task phase timestamps (8 words per task), null when off
+  int64_t* trace;
 };
 int fused_ctl_words(int cb_fs, int cb_h, int cb_f, int max_slots);
 size_t fused_lds_bytes(int B);

@@ -115,31 +115,54 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
   return hipSuccess;
 }
 
-// Control words of the persistent decode kernel, per (device, stream): zeroed
-// once when created; every launch leaves them zero again.
+// Control words of the persistent decode kernel: a per-device arena of
+// kCtlSlots slots, allocated and zeroed by the first call on the device (which
+// must not be under stream capture); each stream takes a slot when first seen
+// (round robin), so no allocation happens later, under capture included.
+// Every launch leaves its slot zero again.  Launches on streams that share a
+// slot must not overlap in time.
 constexpr int kCtlWords = 1 << 14;
-std::map<std::pair<int, hipStream_t>, uint32_t*> g_ctl;
+constexpr int kCtlSlots = 16;
+struct CtlArena {
+  uint32_t* base = nullptr;
+  int next = 0;
+  std::map<hipStream_t, int> slot;
+};
+std::map<int, CtlArena> g_ctl;
 
 hipError_t ctl_words(hipStream_t stream, uint32_t** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  uint32_t*& p = g_ctl[{dev, stream}];
-  if (p == nullptr) {
-    e = hipMalloc(&p, kCtlWords * sizeof(uint32_t));
+  CtlArena& a = g_ctl[dev];
+  if (a.base == nullptr) {
+    e = hipMalloc(&a.base, (size_t)kCtlSlots * kCtlWords * sizeof(uint32_t));
     if (e != hipSuccess) {
-      p = nullptr;
+      a.base = nullptr;
       return e;
     }
-    e = launch_zero_words(p, kCtlWords, stream);
+    e = launch_zero_words(a.base, kCtlSlots * kCtlWords, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return e;
   }
-  *out = p;
+  auto it = a.slot.find(stream);
+  int k;
+  if (it == a.slot.end()) {
+    k = a.next++ % kCtlSlots;
+    a.slot[stream] = k;
+  } else {
+    k = it->second;
+  }
+  *out = a.base + (size_t)k * kCtlWords;
   return hipSuccess;
 }
 
 std::map<std::pair<int, int>, int> g_fused_grid;  // (device, B) -> workgroups
+
+// Optional phase trace of the next persistent decode launch (diagnostics).
+int64_t* g_trace = nullptr;
+int64_t g_trace_words = 0;
 
 hipError_t fused_grid_cached(int B, int* grid) {
   int dev = 0;
@@ -521,6 +544,13 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
     a.sh_down = L->shared_down;
     a.x = x;
     a.out = out;
+    {
+      std::lock_guard<std::mutex> lock(g_ws_mu);
+      if (g_trace != nullptr && g_trace_words >= (int64_t)a.n_tasks * 8) {
+        a.trace = g_trace;
+        g_trace = nullptr;
+      }
+    }
     e = launch_decode_fused(a, grid, s);
     if (e == hipSuccess && expert_ids)
       e = hipMemcpyAsync(expert_ids, a.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
@@ -766,6 +796,20 @@ int uocr_moe_timing_end(int capacity, float* ms, char* names, size_t name_stride
   return 0;
 }
 
+int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err, size_t errlen) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  g_trace = static_cast<int64_t*>(buffer);
+  g_trace_words = words;
+  if (grid_waves) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    *grid_waves = 0;
+    for (auto& kv : g_fused_grid)
+      if (kv.first.first == dev) *grid_waves = kv.second * 4;
+  }
+  return 0;
+}
+
 int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen) {
   uint32_t* ctl = nullptr;
   hipError_t e = ctl_words((hipStream_t)stream, &ctl);
@@ -783,7 +827,7 @@ void uocr_moe_release(void) {
     if (kv.second.ptr != nullptr) (void)hipFree(kv.second.ptr);
   g_ws.clear();
   for (auto& kv : g_ctl)
-    if (kv.second != nullptr) (void)hipFree(kv.second);
+    if (kv.second.base != nullptr) (void)hipFree(kv.second.base);
   g_ctl.clear();
 }
 
