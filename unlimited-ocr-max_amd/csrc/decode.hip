@@ -8,31 +8,41 @@
 // 128-element chunk added in chunk order; SwiGLU; the routing-weighted fma
 // combine plus the shared experts.
 //
-// Work decomposition.  The layer is a list of tasks; task i belongs to wave
-// i mod (number of waves), and every wave walks its tasks in order:
-//   router     one expert's logits for every token          (E tasks)
-//   sgu        shared gate or up, 64 columns x one chunk     (Fs/64 x 2 x H/128)
-//   rgu        routed gate or up of one selected expert,
-//              64 columns x one chunk                        (slots x F/64 x 2 x H/G)
-//   sdn        shared down, 64 columns x one chunk           (H/64 x Fs/128)
-//   rdn        routed down, 64 columns x one chunk           (slots x H/64 x F/G)
-// A chunk task streams a 64-row x 128-byte weight tile with coalesced 16-byte
-// loads (8 lanes per 128-byte line), transposes it through LDS so each lane
-// holds one weight row, runs the bit-exact chain for every token row of its
-// expert, and stores the chain results (plus the group scale) as partials.
-// The task that completes a unit's last chunk (an atomic counter) folds the
-// partials in chunk order: SwiGLU for gate/up, the combine for the last down
-// unit of a column block.  The last router task computes the softmax, top-k
-// and expert grouping.  A task only ever waits on tasks with smaller indices,
-// and every wave of the grid is resident (the grid is sized to the occupancy),
-// so the waits end; each wait is also bounded and records an error if it
-// ever runs out.  The next task's weight tile is loaded into registers while
-// the current one is computed.
+// Work decomposition.  One workgroup of 16 waves per CU; the layer is a list of
+// tasks dealt round robin to the waves (task t to the wave of rank t mod
+// waves, ranks interleaved across workgroups so neighbouring tasks land on
+// different CUs and XCDs), every wave walking its tasks in increasing order:
+//   router  one expert's logits for every token                       (E)
+//   sgu     shared gate or up: 64 columns x one 128-chunk of H         (Fs/64 x 2 x H/128)
+//   rgu     routed gate+up of one selected expert: a few columns,
+//           every chunk of H (lane = column, projection, chunk)        (experts x F/c_gu)
+//   sfold   shared gate/up partials of 64 columns -> SwiGLU -> hs      (Fs/64)
+//   sdn     shared down: 64 columns x one 128-chunk of Fs              (H/64 x Fs/128)
+//   rdn     routed down of one selected expert: a few columns, every
+//           chunk of F (lane = column, chunk)                          (experts x H/c_dn)
+//   comb    64 columns: shared-down partials -> sh, then the weighted
+//           combine of the routed rows plus sh                         (H/64)
+// A routed task holds every chunk of its columns, so its per-group fold runs
+// inside the wave (lane shuffles); only the shared experts, whose chunks are
+// spread over tasks, fold partials written by other waves.  Each lane loads
+// the weights of its own row and chunk (128 int8 or 256 bf16 bytes, 16 bytes
+// per load) straight into registers; 16 waves per CU keep enough loads in
+// flight without a software pipeline.
 //
-// Cross-workgroup data (partials, h, y, routing tables) is written and read
-// with device-coherent (agent-scope) accesses, and every counter update waits
-// for the wave's earlier stores first.  The control counters live in a
-// library-owned buffer that the last wave of a launch resets to zero.
+// Synchronisation.  Every value one wave hands to another (logits, partials,
+// h, hs, y) is stored as a 64-bit pair (fp32 bits, launch tag) with one
+// device-coherent store, and the consumer polls the pairs it needs until all
+// carry the tag of the current launch: no counters and no fences on the data
+// path.  Each workgroup computes the routing itself from the tagged logits.
+// A task waits only on tasks with smaller indices and every workgroup of the
+// grid is resident (the grid is sized to the occupancy), so the waits end;
+// each wait is also bounded and records an error if it ever runs out.  The
+// launch tag is the control word EPOCH + 1: every wave reads EPOCH at its
+// start, each workgroup then adds one to ARRIVED (a non-returning atomic),
+// and the last of the comb tasks (the only counter, H/64 increments) waits
+// for ARRIVED to reach the grid, clears both counters and advances EPOCH.
+// The tagged buffers and control words are library-owned and zeroed when
+// allocated; tags start at 1, so no zeroed word is ever taken for data.
 #include "uocr_device.h"
 #include "uocr_kernels.h"
 
@@ -40,724 +50,749 @@ namespace uocr {
 
 namespace {
 
-constexpr int kWavesPerWg = 4;
-constexpr int kTileRow = 144;   // LDS bytes per weight row of a tile (128 + 16 pad)
-constexpr int kTileBytes = 64 * kTileRow;
-constexpr uint32_t kSpinLimit = 1u << 21;
+constexpr int kWaves = kFusedWaves;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kXPad = kFusedXPad;
+constexpr uint32_t kSpinLimit = 1u << 16;  // polls per wait (tens of ms): real waits take microseconds
 
-// ctl word indices
-constexpr int C_DONE = 0, C_ROUTER = 1, C_READY = 2, C_HS = 3, C_ERR = 4, C_BASE = 8;
+// control words
+constexpr int C_EPOCH = 0, C_ARRIVED = 1, C_COMBINED = 2, C_ERR = 4;
 
-__device__ __forceinline__ float ld_dev(const float* p) {
+// Lane index through a volatile asm: recomputed where it is used, so that the
+// compiler does not hoist lane-derived values (shuffle addresses, masks) out
+// of the task loop and keep them live across every task.
+__device__ __forceinline__ int lane() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// v of lane src (0..63).
+__device__ __forceinline__ float shfl(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ uint32_t shfl(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)v);
+}
+__device__ __forceinline__ uint64_t shfl(uint64_t v, int src) {
+  return ((uint64_t)shfl((uint32_t)(v >> 32), src) << 32) | shfl((uint32_t)v, src);
+}
+
+// Halving-tree sum over the 64 lanes, v[l] += v[l + off] for off = 32..1;
+// lane 0 ends with the total (lanes past the wave read their own value, which
+// is never used).
+__device__ __forceinline__ float tree_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const int l = lane();
+    v = v + shfl(v, l + off < kWave ? l + off : l);
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint32_t ld_word(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int ld_dev(const int* p) {
+__device__ __forceinline__ void st_word(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_pair(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_pair(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ float pair_value(uint64_t q) { return __uint_as_float((uint32_t)q); }
+__device__ __forceinline__ bool pair_has(uint64_t q, uint32_t tag) { return (uint32_t)(q >> 32) == tag; }
+
+// One round of a bounded poll: true once every lane is ready.  After
+// kSpinLimit rounds, or once another wait has failed (the error word, read
+// every 256 rounds), it records an error and lets the wave go on: its results
+// are then wrong, but the launch ends.
+__device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* ctl) {
+  if (__all(ready)) return true;
+  ++spin;
+  if (spin > kSpinLimit || ((spin & 255u) == 0u && ld_word(ctl + C_ERR) != 0u)) {
+    if (lane() == 0) st_word(ctl + C_ERR, 1u);
+    return true;
+  }
+  __builtin_amdgcn_s_sleep(1);
+  return false;
 }
 
-// Waits for this wave's earlier stores, then adds 1 to a counter; returns the
-// old value in every lane.
-__device__ __forceinline__ uint32_t signal(uint32_t* c) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  uint32_t old = 0;
-  if (lane_id() == 0) old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __shfl(old, 0, kWave);
-}
-
-// Spins until *c >= target; on running out of spins, records an error and
-// returns (the results of such a launch are wrong, but it ends).
-__device__ void wait_ge(uint32_t* ctl, int idx, uint32_t target) {
-  for (uint32_t spin = 0;; ++spin) {
-    if (ld_dev(ctl + idx) >= target) return;
-    if (spin > kSpinLimit) {
-      if (lane_id() == 0) st_dev(ctl + C_ERR, 1u);
-      return;
+// Polls n tagged pairs p[i * stride] (i < n <= N, per lane) until all carry
+// `tag`; their values land in v[0..n).  The addresses advance from p (no
+// per-index offsets for the compiler to hoist out of the task loop).
+template <int N>
+__device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, uint32_t* ctl,
+                                           float (&v)[N]) {
+  uint32_t spin = 0;
+  for (;;) {
+    uint64_t q[N];
+    const uint64_t* a = p;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      q[i] = ld_pair(a);
+      if (i + 1 < n) a += stride;
     }
-    __builtin_amdgcn_s_sleep(2);
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      v[i] = pair_value(q[i]);
+      ok = ok && pair_has(q[i], tag);
+    }
+    if (poll_done(ok, spin, ctl)) return;
   }
 }
 
-// The same pointer, asserted wave-uniform (both halves through readfirstlane).
-__device__ __forceinline__ const float* uniform_ptr(const float* p) {
-  const uint64_t u = (uint64_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-  return (const float*)(((uint64_t)hi << 32) | lo);
-}
+// x / d for 0 <= x < 2^16 and 1 <= d <= 64, from inv = 1/d: (x + 1/2)/d stays
+// at least 1/(2d) away from the next integer, far beyond the rounding error.
+__device__ __forceinline__ int small_div(int x, float inv) { return (int)(((float)x + 0.5f) * inv); }
 
-// Rows a chain template covers for B rows (1, 2, 4 or 8): the activation stage
-// holds that many rows so padded rows read inside it.
-__host__ __device__ constexpr int padded_rows(int B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
-
-// Phase timestamps of a task (the constant-rate wall clock), when tracing.
-#define UOCR_TRACE(a, task, slot)                                                    \
-  do {                                                                               \
-    if ((a).trace != nullptr && lane_id() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
+#define UOCR_TRACE(a, task, slot)                                                                          \
+  do {                                                                                                     \
+    if ((a).trace != nullptr && lane() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
   } while (0)
 
-enum TaskKind : int { T_ROUTER = 0, T_SGU = 1, T_RGU = 2, T_SDN = 3, T_RDN = 4, T_NONE = 5 };
+// --------------------------------------------------------------------------- tasks
+
+enum Kind : int { K_ROUTER, K_SGU, K_RGU, K_SFOLD, K_SDN, K_RDN, K_COMB, K_NONE };
 
 struct Task {
   int kind;
-  int slot;   // routed expert slot (group index)
-  int cb;     // 64-column block
-  int p;      // 0 gate, 1 up (gate/up tasks)
-  int c;      // chunk
-  int e;      // router: expert
+  int a;  // router: expert; sgu/sfold: column block of Fs; rgu/rdn: expert slot; sdn/comb: column block of H
+  int b;  // sgu: projection; rgu/rdn: column group; sdn: chunk of Fs
+  int c;  // sgu: chunk of H
 };
 
-__device__ __forceinline__ Task decode_task(const FusedArgs& a, int t) {
-  Task k{T_NONE, 0, 0, 0, 0, 0};
-  if (t < a.n_router) {
-    k.kind = T_ROUTER;
-    k.e = t;
-    return k;
-  }
-  t -= a.n_router;
-  if (t < a.n_sgu) {
-    k.kind = T_SGU;
-    const int per_unit = 2 * a.ch_h;
-    k.cb = t / per_unit;
-    const int r = t - k.cb * per_unit;
-    k.p = r / a.ch_h;
-    k.c = r - k.p * a.ch_h;
-    return k;
-  }
-  t -= a.n_sgu;
-  if (t < a.n_rgu) {
-    k.kind = T_RGU;
-    const int per_unit = 2 * a.ch_h;
-    const int unit = t / per_unit;
-    const int r = t - unit * per_unit;
-    k.slot = unit / a.cb_f;
-    k.cb = unit - k.slot * a.cb_f;
-    k.p = r / a.ch_h;
-    k.c = r - k.p * a.ch_h;
-    return k;
-  }
-  t -= a.n_rgu;
-  if (t < a.n_sdn) {
-    k.kind = T_SDN;
-    k.cb = t / a.ch_fs;
-    k.c = t - k.cb * a.ch_fs;
-    return k;
-  }
-  t -= a.n_sdn;
-  if (t < a.n_rdn) {
-    k.kind = T_RDN;
-    const int unit = t / a.ch_f;
-    k.c = t - unit * a.ch_f;
-    k.slot = unit / a.cb_h;
-    k.cb = unit - k.slot * a.cb_h;
-    return k;
-  }
-  return k;
+__device__ __forceinline__ int task_count(const FusedArgs& A, int ng) {
+  return A.E + A.n_sgu + ng * A.per_e_gu + A.cb_fs + A.n_sdn + ng * A.per_e_dn + A.cb_h;
 }
 
-// --------------------------------------------------------------------------- weight tiles
+__device__ __forceinline__ Task task_at(const FusedArgs& A, int ng, int t) {
+  if (t < A.E) return {K_ROUTER, t, 0, 0};
+  t -= A.E;
+  if (t < A.n_sgu) {
+    const int per_u = 2 * A.gh;
+    const int u = t / per_u;
+    const int r = t - u * per_u;
+    const int p = r / A.gh;
+    return {K_SGU, u, p, r - p * A.gh};
+  }
+  t -= A.n_sgu;
+  if (t < ng * A.per_e_gu) {
+    const int s = t / A.per_e_gu;
+    return {K_RGU, s, t - s * A.per_e_gu, 0};
+  }
+  t -= ng * A.per_e_gu;
+  if (t < A.cb_fs) return {K_SFOLD, t, 0, 0};
+  t -= A.cb_fs;
+  if (t < A.n_sdn) {
+    const int cb = t / A.gfs;
+    return {K_SDN, cb, t - cb * A.gfs, 0};
+  }
+  t -= A.n_sdn;
+  if (t < ng * A.per_e_dn) {
+    const int s = t / A.per_e_dn;
+    return {K_RDN, s, t - s * A.per_e_dn, 0};
+  }
+  t -= ng * A.per_e_dn;
+  if (t < A.cb_h) return {K_COMB, t, 0, 0};
+  return {K_NONE, 0, 0, 0};
+}
 
-// Registers holding one task's weight tile(s) in flight: up to 2 sub-tiles
-// of 64 rows x 128 bytes, 8 x 16 bytes per lane each.
-struct Stage {
-  i32x4 v[2][8];
+// --------------------------------------------------------------------------- routing
+
+// The routing as every wave holds it: lane r (< B*topk) has routed row r's
+// expert, `mask` the selected experts, ng their number.  Slot s is the s-th
+// selected expert in ascending id.
+struct Route {
+  int my_id;
+  uint64_t mask;
+  int ng;
 };
 
-// Issues the loads of one 64x128-byte sub-tile of a row-major [N, Kbytes]
-// matrix (rows n0.., bytes kb0..kb0+127): instruction i, lane l -> row
-// n0 + 8i + l/8, bytes (l%8)*16.  Rows past N repeat row N-1.
-__device__ __forceinline__ void issue_rows(i32x4 (&v)[8], const char* base, int64_t row_bytes, int n0, int N,
-                                           int64_t kb0) {
-  const int l = lane_id();
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int n = min(n0 + 8 * i + (l >> 3), N - 1);
-    v[i] = *(const UOCR_GLOBAL i32x4*)(base + (int64_t)n * row_bytes + kb0 + (l & 7) * 16);
-  }
+__device__ __forceinline__ int slot_expert(const Route& rt, int s) {
+  const int l = lane();
+  const bool bit = ((rt.mask >> l) & 1ull) != 0ull;
+  const int prefix = __builtin_popcountll(rt.mask & ((1ull << l) - 1ull));
+  const uint64_t b = __ballot(bit && prefix == s);
+  return (int)__builtin_ctzll(b);
 }
 
-// The same for a K-blocked bf16 [K/16, N, 16] matrix: the sub-tile is 64 rows
-// x 64 elements (K blocks kb0..kb0+3); instruction i, lane l -> block
-// kb0 + i/2, row n0 + 32*(i%2) + l/2, half l%2.
-__device__ __forceinline__ void issue_kblocked(i32x4 (&v)[8], const uint16_t* w, int N, int n0, int kb0) {
-  const int l = lane_id();
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int kb = kb0 + (i >> 1);
-    const int n = min(n0 + 32 * (i & 1) + (l >> 1), N - 1);
-    v[i] = *(const UOCR_GLOBAL i32x4*)(w + ((int64_t)kb * N + n) * 16 + (l & 1) * 8);
-  }
-}
+// Routed rows of expert e, ascending (a bit per row).
+__device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) { return __ballot(rt.my_id == e); }
 
-// Writes a staged sub-tile to the wave's LDS tile in row order (row r at
-// r*kTileRow, 16-byte piece q at q*16).
-__device__ __forceinline__ void tile_store(char* tile, const i32x4 (&v)[8], bool kblocked) {
-  const int l = lane_id();
+// Softmax + top-k of token t from its tagged logits into the workgroup's
+// tables (same steps as route.hip's k_softmax_topk), then one more on the
+// workgroup's count of routed tokens.
+__device__ __attribute__((always_inline)) void route_token(const FusedArgs& A, int t, uint32_t tag, int* r_ids,
+                                                           float* r_wts, int* r_done) {
+  const int l = lane();
+  const uint64_t* src = A.logits + t * 64 + (l < A.E ? l : A.E - 1);
+  uint64_t q;
+  uint32_t spin = 0;
+  do {
+    q = ld_pair(src);
+  } while (!poll_done(pair_has(q, tag), spin, A.ctl));
+  const float v = l < A.E ? pair_value(q) : -__builtin_huge_valf();
+  float m = v;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int r, q;
-    if (kblocked) {
-      r = 32 * (i & 1) + (l >> 1);
-      q = (i >> 1) * 2 + (l & 1);
-    } else {
-      r = 8 * i + (l >> 3);
-      q = l & 7;
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, shfl(m, lane() ^ off));
+  const float ex = l < A.E ? uexp(v - m) : 0.0f;
+  const float S = shfl(tree_sum(ex), 0);
+  const float pr = l < A.E ? ex / S : 0.0f;
+  uint64_t key = l < A.E ? (((uint64_t)__float_as_uint(pr) << 32) | (uint64_t)(kWave - l)) : 0ull;
+  float d = 0.0f;
+  for (int j = 0; j < A.topk; ++j) {
+    uint64_t best = key;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint64_t o = shfl(best, lane() ^ off);
+      best = o > best ? o : best;
     }
-    *(i32x4*)(tile + r * kTileRow + q * 16) = v[i];
+    const int sel = kWave - (int)(best & 0xFFFFFFFFu);
+    const float ws = shfl(pr, sel);
+    d = d + ws;
+    if (l == sel) key = 0ull;
+    if (l == 0) {
+      r_ids[t * A.topk + j] = sel;
+      r_wts[t * A.topk + j] = ws;
+    }
+  }
+  if (l == 0) {
+    for (int j = 0; j < A.topk; ++j) {
+      const int i = t * A.topk + j;
+      if (A.renorm) r_wts[i] = r_wts[i] / d;
+      if (blockIdx.x == 0) {
+        if (A.ids_out != nullptr) A.ids_out[i] = r_ids[i];
+        if (A.wts_out != nullptr) A.wts_out[i] = r_wts[i];
+      }
+    }
+    // the tables are in LDS before the count says so
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __hip_atomic_fetch_add(r_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+__device__ __forceinline__ Route make_route(const FusedArgs& A, const int* r_ids) {
+  const int l = lane();
+  Route rt;
+  rt.my_id = l < A.B * A.topk ? r_ids[l] : -1;
+  uint64_t bit = rt.my_id >= 0 ? (1ull << rt.my_id) : 0ull;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) bit |= shfl(bit, lane() ^ off);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bit);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(bit >> 32));
+  rt.mask = ((uint64_t)hi << 32) | lo;
+  rt.ng = __builtin_popcountll(rt.mask);
+  return rt;
+}
+
+// --------------------------------------------------------------------------- weights
+
+// The lane's weights of one task: its row's chunk as 16-byte pieces in k
+// order, 8 pieces of 16 int8 or 16 pieces of 8 bf16.
+template <bool INT8>
+struct Stage {
+  i32x4 v[INT8 ? 8 : 16];
+};
+
+__device__ __forceinline__ i32x4 ld16(const void* p) { return *(const UOCR_GLOBAL i32x4*)p; }
+
+// A routed expert task: lane l is (column c, projection p, chunk g) =
+// ((2c + p) * gh + g) for gate/up, (c * gf + g) for down, and loads its 128
+// (int8) or 256 (bf16) contiguous bytes; lanes past the task repeat its last
+// lane's row.
+template <bool INT8>
+__device__ __attribute__((always_inline)) void issue_routed(const FusedArgs& A, bool gu, int e, int n0, int ncols,
+                                                            Stage<INT8>& st) {
+  const int l = lane();
+  const int G = gu ? A.gh : A.gf;
+  const int N = gu ? A.F : A.H;
+  constexpr int64_t esz = INT8 ? 1 : 2;
+  const int lam = min(l, (gu ? 2 : 1) * ncols * G - 1);
+  const int cp = small_div(lam, gu ? A.inv_gh : A.inv_gf);
+  const int g = lam - cp * G;
+  const int c = gu ? cp >> 1 : cp;
+  const char* w = (const char*)(gu ? ((cp & 1) ? A.up_w : A.gate_w) : A.down_w);
+  const char* p = w + (((int64_t)e * N + n0 + c) * (gu ? A.H : A.F) + (int64_t)g * 128) * esz;
+#pragma unroll
+  for (int i = 0; i < (INT8 ? 8 : 16); ++i) st.v[i] = ld16(p + 16 * i);
+}
+
+// A shared task (K-blocked bf16 [K/16, N, 16]): lane l is column n0 + l and
+// loads chunk g, K-blocks 8g..8g+7, 32 bytes each.
+__device__ __forceinline__ void issue_kblocked(const uint16_t* w, int N, int n0, int g, Stage<false>& st) {
+  const uint16_t* p = w + ((int64_t)(8 * g) * N + n0 + lane()) * 16;
+  const int64_t block = (int64_t)N * 16;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    st.v[i] = ld16(p);
+    st.v[i + 1] = ld16(p + 8);
+    p += block;
   }
 }
 
 // ---------------------------------------------------------------------------- chains
 
-// Activation access: scalar loads of the kernel input x, or LDS broadcast of
-// an activation staged by the wave (h, hs: produced inside the kernel).
-struct XSrc {
-  const float* row[8];   // x rows (global) when from_lds == false
-  const float* lds;      // staged rows, row r at lds + r * 128, when from_lds
-  bool from_lds;
-};
-
-
-// Elements of the chunk handled per step: 16, or 8 for 8 rows (the x values
-// of a step live in scalar registers).
-template <int R, bool LDSX>
-constexpr int kStep = LDSX ? 4 : (R > 4 ? 8 : 16);
-
-// x[r][k..k+S-1] of every row r < R into registers: scalar loads of the kernel
-// input, or LDS broadcasts of a staged activation.
-template <int R, int S, bool LDSX>
-__device__ __forceinline__ void load_x(const XSrc& xs, int k, float (&xv)[8][16]) {
+// The fp32 chain of one row over the lane's chunk, in k order: acc =
+// fma(w_k, x_k, acc) from 0, x_k at xp[k] (LDS).  The activations of piece
+// q+1 are read while piece q is computed; their offset passes through an
+// empty asm that takes the accumulator, so the read cannot be issued before
+// piece q-1 is done and the scheduler cannot hoist every read (128 floats)
+// to the top.  Callers run it once per row: a second empty asm makes each
+// piece's weights opaque so that the compiler widens them inside the row loop
+// instead of hoisting all of them out of it.
+template <bool INT8>
+__device__ __forceinline__ float chain(const Stage<INT8>& st, const float* xp) {
+  constexpr int NP = INT8 ? 8 : 16;  // pieces
+  constexpr int EP = INT8 ? 16 : 8;  // elements per piece
+  constexpr int NV = EP / 4;         // 4-float LDS reads per piece
+  float acc = 0.0f;
+  f32x4 cur[NV];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if constexpr (LDSX) {
+  for (int v = 0; v < NV; ++v) cur[v] = *(const f32x4*)(xp + 4 * v);
 #pragma unroll
-      for (int v = 0; v < S / 4; ++v) {
-        const f32x4 q = *(const f32x4*)(xs.lds + r * 128 + k + 4 * v);
-        xv[r][4 * v] = q.x;
-        xv[r][4 * v + 1] = q.y;
-        xv[r][4 * v + 2] = q.z;
-        xv[r][4 * v + 3] = q.w;
+  for (int q = 0; q < NP; ++q) {
+    f32x4 nxt[NV];
+    if (q + 1 < NP) {
+      int off = (q + 1) * EP;
+      asm volatile("" : "+v"(off) : "v"(acc));
+#pragma unroll
+      for (int v = 0; v < NV; ++v) nxt[v] = *(const f32x4*)(xp + off + 4 * v);
+    }
+    i32x4 wq = st.v[q];
+    asm volatile("" : "+v"(wq));
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * v + j;
+        if constexpr (INT8)
+          w[j] = (float)(int8_t)((uint32_t)wq[e >> 2] >> (8 * (e & 3)));
+        else
+          w[j] = (e & 1) ? bf16_hi((uint32_t)wq[e >> 1]) : bf16_lo((uint32_t)wq[e >> 1]);
       }
-    } else {
+      acc = __builtin_fmaf(w[0], cur[v].x, acc);
+      acc = __builtin_fmaf(w[1], cur[v].y, acc);
+      acc = __builtin_fmaf(w[2], cur[v].z, acc);
+      acc = __builtin_fmaf(w[3], cur[v].w, acc);
+    }
+    if (q + 1 < NP) {
 #pragma unroll
-      for (int j = 0; j < S; ++j) xv[r][j] = ldc(xs.row[r] + k + j);
+      for (int v = 0; v < NV; ++v) cur[v] = nxt[v];
     }
   }
+  return acc;
 }
 
-// One int8 sub-tile: the lane's 128 weights of its row, chained per token row
-// into part[] in k order.
-template <int R, bool LDSX>
-__device__ __forceinline__ void chain_int8(const char* tile, const XSrc& xs, float (&part)[8]) {
-  constexpr int S = kStep<R, LDSX>;
-  const int l = lane_id();
-#pragma unroll 1
-  for (int k0 = 0; k0 < 128; k0 += S) {
-    const i32x4 wq = *(const i32x4*)(tile + l * kTileRow + (k0 & ~15));
-    float xv[8][16];
-    load_x<R, S, LDSX>(xs, k0, xv);
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const int kk = (k0 & 15) + j;  // byte of the 16-byte piece
-      const float wv = (float)(int8_t)(wq[kk >> 2] >> (8 * (kk & 3)));
-#pragma unroll
-      for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf(wv, xv[r][j], part[r]);
-    }
-  }
-}
+// ----------------------------------------------------------------------------- tasks
 
-// One bf16 sub-tile: the lane's 64 weights of its row (k = koff..koff+63).
-template <int R, bool LDSX>
-__device__ __forceinline__ void chain_bf16(const char* tile, const XSrc& xs, int koff, float (&part)[8]) {
-  constexpr int S = kStep<R, LDSX>;
-  const int l = lane_id();
-#pragma unroll 1
-  for (int k0 = 0; k0 < 64; k0 += S) {
-    float xv[8][16];
-    load_x<R, S, LDSX>(xs, koff + k0, xv);
-    // 16-byte pieces of 8 bf16 covering the step
-    constexpr int NP = S >= 8 ? S / 8 : 1;
-    i32x4 wq[NP];
-#pragma unroll
-    for (int pc = 0; pc < NP; ++pc) wq[pc] = *(const i32x4*)(tile + l * kTileRow + ((k0 & ~7) + 8 * pc) * 2);
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const int kk = (k0 & 7) + j;  // element counted from the first piece
-      const uint32_t word = (uint32_t)wq[kk >> 3][(kk & 7) >> 1];
-      const float wv = (kk & 1) == 0 ? bf16_lo(word) : bf16_hi(word);
-#pragma unroll
-      for (int r = 0; r < R; ++r) part[r] = __builtin_fmaf(wv, xv[r][j], part[r]);
-    }
-  }
-}
-
-template <int R, bool LDSX>
-__device__ __forceinline__ void run_chain(bool int8, int subtiles, char* tile, const Stage& st, bool kblocked,
-                                          const XSrc& xs, float (&part)[8]) {
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    if (s >= subtiles) break;
-    tile_store(tile, st.v[s], kblocked);
-    __builtin_amdgcn_wave_barrier();
-    if (int8)
-      chain_int8<R, LDSX>(tile, xs, part);
-    else
-      chain_bf16<R, LDSX>(tile, xs, s * 64, part);
-    __builtin_amdgcn_wave_barrier();
-  }
-}
-
-template <bool LDSX>
-__device__ __forceinline__ void run_chain_rows(int R, bool int8, int subtiles, char* tile, const Stage& st,
-                                               bool kblocked, const XSrc& xs, float (&part)[8]) {
-  if (R <= 1)
-    run_chain<1, LDSX>(int8, subtiles, tile, st, kblocked, xs, part);
-  else if (R <= 2)
-    run_chain<2, LDSX>(int8, subtiles, tile, st, kblocked, xs, part);
-  else if (R <= 4)
-    run_chain<4, LDSX>(int8, subtiles, tile, st, kblocked, xs, part);
-  else
-    run_chain<8, LDSX>(int8, subtiles, tile, st, kblocked, xs, part);
-}
-
-// ---------------------------------------------------------------------------- the kernel
-
-struct Wave {
-  char* tile;     // kTileBytes
-  float* xstage;  // B * 128 floats
+struct Ctx {
+  const float* xs;  // x rows in LDS, row t at t * gh * kXPad, chunk g at + g * kXPad
+  const int* r_ids;
+  const float* r_wts;
+  float* act;       // the wave's activation stage
+  uint32_t tag;
 };
 
-__device__ __forceinline__ uint32_t* ctl_sgu(const FusedArgs& a) { return a.ctl + C_BASE; }
-__device__ __forceinline__ uint32_t* ctl_hready(const FusedArgs& a) { return a.ctl + C_BASE + a.cb_fs; }
-__device__ __forceinline__ uint32_t* ctl_sdn(const FusedArgs& a) { return ctl_hready(a) + 64; }
-__device__ __forceinline__ uint32_t* ctl_out(const FusedArgs& a) { return ctl_sdn(a) + a.cb_h; }
-__device__ __forceinline__ uint32_t* ctl_rgu(const FusedArgs& a) { return ctl_out(a) + a.cb_h; }
-__device__ __forceinline__ uint32_t* ctl_rdn(const FusedArgs& a) { return ctl_rgu(a) + a.max_slots * a.cb_f; }
-
-__device__ __forceinline__ bool routing_ready(const FusedArgs& a) { return ld_dev(a.ctl + C_READY) != 0u; }
-
-// Loads the weight tile(s) of a chunk task into registers.  Routed tasks need
-// the routing; returns false for a routed slot beyond the selected experts.
-__device__ __attribute__((always_inline)) bool issue_task(const FusedArgs& a, const Task& k, Stage& st) {
-  if (k.kind == T_SGU) {
-    const uint16_t* w = k.p == 0 ? a.sh_gate : a.sh_up;
-    issue_kblocked(st.v[0], w, a.Fs, k.cb * 64, k.c * 8);
-    issue_kblocked(st.v[1], w, a.Fs, k.cb * 64, k.c * 8 + 4);
-    return true;
-  }
-  if (k.kind == T_SDN) {
-    issue_kblocked(st.v[0], a.sh_down, a.H, k.cb * 64, k.c * 8);
-    issue_kblocked(st.v[1], a.sh_down, a.H, k.cb * 64, k.c * 8 + 4);
-    return true;
-  }
-  if (k.kind == T_RGU || k.kind == T_RDN) {
-    if (k.slot >= ld_dev(a.n_groups)) return false;
-    const int e = ld_dev(a.group_expert + k.slot);
-    const bool gu = k.kind == T_RGU;
-    const char* w = (const char*)(gu ? (k.p == 0 ? a.gate_w : a.up_w) : a.down_w);
-    const int N = gu ? a.F : a.H;
-    const int K = gu ? a.H : a.F;
-    if (a.int8) {
-      issue_rows(st.v[0], w + (int64_t)e * N * K, K, k.cb * 64, N, (int64_t)k.c * 128);
-    } else {
-      const int64_t rb = (int64_t)K * 2;
-      issue_rows(st.v[0], w + (int64_t)e * N * rb, rb, k.cb * 64, N, (int64_t)k.c * 256);
-      issue_rows(st.v[1], w + (int64_t)e * N * rb, rb, k.cb * 64, N, (int64_t)k.c * 256 + 128);
-    }
-    return true;
-  }
-  return false;
-}
-
-// router task: logits[t][e] for every token t of the step (H <= 2048): the
-// lane's router values and each token's x values are loaded in one batch.
-constexpr int kMaxHPerLane = 32;
-
-__device__ __attribute__((always_inline)) void router_task(const FusedArgs& a, int e) {
-  const int l = lane_id();
-  const float* wr = a.router + (int64_t)e * a.H;
-  const int nk = (a.H - l + kWave - 1) / kWave;  // k = l + 64j, j < nk
-  float w[kMaxHPerLane];
+__device__ __attribute__((always_inline)) void router_task(const FusedArgs& A, const Ctx& C, int e) {
+  constexpr int kMaxJ = 32;  // H <= 2048
+  const int l = lane();
+  const float* wr = A.router + (int64_t)e * A.H;
+  const int nk = A.H / kWave;  // k = l + 64 j
+  float w[kMaxJ];
 #pragma unroll
-  for (int j = 0; j < kMaxHPerLane; ++j) w[j] = j < nk ? ldg(wr + l + kWave * j) : 0.0f;
-  for (int t = 0; t < a.B; ++t) {
-    const float* xr = a.x + (int64_t)t * a.H + l;
-    float xv[kMaxHPerLane];
-#pragma unroll
-    for (int j = 0; j < kMaxHPerLane; ++j) xv[j] = j < nk ? ldg(xr + kWave * j) : 0.0f;
+  for (int j = 0; j < kMaxJ; ++j) w[j] = j < nk ? ldg(wr + l + kWave * j) : 0.0f;
+  for (int t = 0; t < A.B; ++t) {
+    const float* xr = C.xs + t * A.gh * kXPad + l;
     float p = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxHPerLane; ++j)
-      if (j < nk) p = __builtin_fmaf(xv[j], w[j], p);
-    const float v = wave_tree_sum(p);
-    if (l == 0) st_dev(a.logits + t * 64 + e, v);
+    for (int j = 0; j < kMaxJ; ++j)
+      if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
+    const float v = tree_sum(p);
+    if (l == 0) st_pair(A.logits + t * 64 + e, v, C.tag);
   }
 }
 
-// The routing (by the last router task): softmax + top-k per token, then the
-// selected (token, slot) rows grouped by expert in ascending expert id, rows
-// ascending within a group.
-__device__ __attribute__((always_inline)) void routing(const FusedArgs& a) {
-  const int l = lane_id();
-  const int R = a.B * a.topk;
-  for (int t = 0; t < a.B; ++t) {
-    const float v = l < a.E ? ld_dev(a.logits + t * 64 + l) : -__builtin_huge_valf();
-    float m = v;
+// Shared gate or up, 64 columns x chunk g of H, every token: partials.
+__device__ __attribute__((always_inline)) void sgu_rows(const FusedArgs& A, const Ctx& C, const Task& k,
+                                                        const Stage<false>& st) {
+  uint64_t* dst = A.p_sgu + ((int64_t)(k.a * 2 + k.b) * A.gh + k.c) * A.B * 64 + lane();
+  for (int r = 0; r < A.B; ++r)
+    st_pair(dst + r * 64, chain<false>(st, C.xs + (r * A.gh + k.c) * kXPad), C.tag);
+}
+
+__device__ __attribute__((always_inline)) void task_sgu(const FusedArgs& A, const Ctx& C, const Task& k) {
+  Stage<false> st;
+  issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
+  sgu_rows(A, C, k, st);
+}
+
+// Shared gate/up fold of 64 columns: hs = silu(sum_g gate) * (sum_g up),
+// chunk sums added in order.
+__device__ __attribute__((always_inline)) void task_sfold(const FusedArgs& A, const Ctx& C, const Task& k) {
+  constexpr int kMaxG = 16;
+  const int l = lane();
+  const int n = k.a * 64 + l;
+  for (int r = 0; r < A.B; ++r) {
+    float acc[2];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-    const float ex = l < a.E ? uexp(v - m) : 0.0f;
-    const float S = __shfl(wave_tree_sum(ex), 0, kWave);
-    const float pr = l < a.E ? ex / S : 0.0f;
-    uint64_t key = l < a.E ? (((uint64_t)__float_as_uint(pr) << 32) | (uint64_t)(kWave - l)) : 0ull;
-    float d = 0.0f;
-    for (int j = 0; j < a.topk; ++j) {
-      uint64_t best = key;
+    for (int p = 0; p < 2; ++p) {
+      float v[kMaxG];
+      poll_pairs<kMaxG>(A.p_sgu + ((int64_t)(k.a * 2 + p) * A.gh * A.B + r) * 64 + l, (int64_t)A.B * 64, A.gh,
+                        C.tag, A.ctl, v);
+      float s = 0.0f;
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const uint64_t o = __shfl_xor(best, off, kWave);
-        best = o > best ? o : best;
+      for (int g = 0; g < kMaxG; ++g)
+        if (g < A.gh) s = s + v[g];
+      acc[p] = s;
+    }
+    st_pair(A.hs + (int64_t)r * A.Fs + n, silu(acc[0]) * acc[1], C.tag);
+  }
+}
+
+// Shared down, 64 columns x chunk g of Fs, every token: partials.
+__device__ __attribute__((always_inline)) void task_sdn(const FusedArgs& A, const Ctx& C, const Task& k) {
+  const int l = lane();
+  const int g = k.b;
+  Stage<false> st;
+  issue_kblocked(A.sh_down, A.H, k.a * 64, g, st);
+  // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
+  {
+    // rows r0..r0+3 per round: pair i is row r0 + i/2, element (i%2)*64 + l
+    constexpr int kMaxP = 8;
+    for (int r0 = 0; r0 < A.B; r0 += kMaxP / 2) {
+      const int np = min(kMaxP, 2 * (A.B - r0));
+      const uint64_t* src = A.hs + (int64_t)r0 * A.Fs + (int64_t)g * 128 + l;
+      float v[kMaxP];
+      uint32_t spin = 0;
+      for (;;) {
+        uint64_t q[kMaxP];
+        const uint64_t* a = src;
+#pragma unroll
+        for (int i = 0; i < kMaxP; i += 2) {
+          q[i] = ld_pair(a);
+          q[i + 1] = ld_pair(a + 64);
+          if (i + 2 < np) a += A.Fs;
+        }
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < kMaxP; ++i) {
+          v[i] = pair_value(q[i]);
+          ok = ok && pair_has(q[i], C.tag);
+        }
+        if (poll_done(ok, spin, A.ctl)) break;
       }
-      const int sel = kWave - (int)(best & 0xFFFFFFFFu);
-      const float ws = __shfl(pr, sel, kWave);
-      d = d + ws;
-      if (l == sel) key = 0ull;
-      if (l == 0) {
-        st_dev(a.ids + t * a.topk + j, sel);
-        st_dev(a.wts + t * a.topk + j, ws);
+#pragma unroll
+      for (int i = 0; i < kMaxP; ++i)
+        if (i < np) C.act[(r0 + (i >> 1)) * 128 + (i & 1) * 64 + l] = v[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  uint64_t* dst = A.p_sdn + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
+  for (int r = 0; r < A.B; ++r) st_pair(dst + r * 64, chain<false>(st, C.act + r * 128), C.tag);
+}
+
+// Routed gate+up of one expert for c_gu columns, every chunk of H, the
+// expert's routed rows: h = silu(fold(gate)) * fold(up), fold over the
+// 128-groups in order.
+template <bool INT8>
+__device__ __attribute__((always_inline)) void task_rgu(const FusedArgs& A, const Ctx& C, const Route& rt,
+                                                        const Task& k) {
+  constexpr int kMaxG = 16;
+  const int l = lane();
+  const int e = slot_expert(rt, k.a);
+  uint64_t rows = slot_rows(rt, e);
+  const int n0 = k.b * A.c_gu;
+  const int ncols = min(A.c_gu, A.F - n0);
+  Stage<INT8> st;
+  issue_routed<INT8>(A, true, e, n0, ncols, st);
+  const int lanes = 2 * ncols * A.gh;
+  const int lam = min(l, lanes - 1);
+  const int cp = small_div(lam, A.inv_gh);
+  const int g = lam - cp * A.gh;
+  const int c = cp >> 1;
+  const int base = cp * A.gh;  // first lane of the lane's (column, projection)
+  float sv[INT8 ? kMaxG : 1];
+  if constexpr (INT8) {
+    const float scale = ldg(((cp & 1) ? A.up_s : A.gate_s) + ((int64_t)e * A.F + n0 + c) * A.gh + g);
+#pragma unroll
+    for (int gg = 0; gg < kMaxG; ++gg) sv[gg] = shfl(scale, base + min(gg, A.gh - 1));
+  }
+  const bool writer = (cp & 1) == 0 && g == 0 && l < lanes;
+  while (rows != 0ull) {
+    const int r = (int)__builtin_ctzll(rows);
+    rows &= rows - 1ull;
+    const float part = chain<INT8>(st, C.xs + ((r / A.topk) * A.gh + g) * kXPad);
+    float acc = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < kMaxG; ++gg) {
+      if (gg < A.gh) {
+        const float pv = shfl(part, base + gg);
+        if constexpr (INT8)
+          acc = __builtin_fmaf(sv[gg], pv, acc);
+        else
+          acc = acc + pv;
       }
     }
-    if (a.renorm && l == 0)
-      for (int j = 0; j < a.topk; ++j) st_dev(a.wts + t * a.topk + j, ld_dev(a.wts + t * a.topk + j) / d);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // grouping: lane r holds row r's expert (R <= 64)
-  const int my = l < R ? ld_dev(a.ids + l) : -1;
-  int ng = 0, off = 0;
-  for (int e = 0; e < a.E; ++e) {
-    const uint64_t mask = __ballot(my == e);
-    if (mask == 0ull) continue;
-    if (my == e) {
-      const int rank = __builtin_popcountll(mask & ((1ull << l) - 1ull));
-      st_dev(a.group_rows + off + rank, l);
-    }
-    if (l == 0) {
-      st_dev(a.group_expert + ng, e);
-      st_dev(a.group_start + ng, off);
-    }
-    off += __builtin_popcountll(mask);
-    ++ng;
-  }
-  if (l == 0) {
-    st_dev(a.group_start + ng, off);
-    st_dev(a.n_groups, ng);
+    const float up = shfl(acc, min(l + A.gh, kWave - 1));
+    if (writer) st_pair(A.h + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
   }
 }
 
-// Rows of a unit: tokens (shared) or the routed rows of a group.
-struct Rows8 {
-  int cnt;
-  int row[8];
-};
-
-__device__ __attribute__((always_inline)) Rows8 unit_rows(const FusedArgs& a, const Task& k) {
-  Rows8 r;
-  if (k.kind == T_SGU || k.kind == T_SDN) {
-    r.cnt = a.B;
+// Routed down of one expert for c_dn columns, every chunk of F, row by row:
+// y = fold over the 128-groups in order.
+template <bool INT8>
+__device__ __attribute__((always_inline)) void task_rdn(const FusedArgs& A, const Ctx& C, const Route& rt,
+                                                        const Task& k) {
+  constexpr int kMaxG = 16;
+  constexpr int kMaxP = 8;  // pairs per lane per poll round
+  const int l = lane();
+  const int e = slot_expert(rt, k.a);
+  uint64_t rows = slot_rows(rt, e);
+  const int n0 = k.b * A.c_dn;
+  const int ncols = min(A.c_dn, A.H - n0);
+  Stage<INT8> st;
+  issue_routed<INT8>(A, false, e, n0, ncols, st);
+  const int lanes = ncols * A.gf;
+  const int lam = min(l, lanes - 1);
+  const int c = small_div(lam, A.inv_gf);
+  const int g = lam - c * A.gf;
+  const int base = c * A.gf;
+  float sv[INT8 ? kMaxG : 1];
+  if constexpr (INT8) {
+    const float scale = ldg(A.down_s + ((int64_t)e * A.H + n0 + c) * A.gf + g);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r.row[i] = min(i, a.B - 1);
-  } else {
-    const int s0 = ld_dev(a.group_start + k.slot);
-    r.cnt = ld_dev(a.group_start + k.slot + 1) - s0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r.row[i] = __builtin_amdgcn_readfirstlane(ld_dev(a.group_rows + s0 + min(i, r.cnt - 1)));
+    for (int gg = 0; gg < kMaxG; ++gg) sv[gg] = shfl(scale, base + min(gg, A.gf - 1));
   }
-  return r;
-}
-
-// Stages activation rows (produced in this kernel) for a chunk: rows
-// src[row*ld + k0 .. +128), every load issued before the first LDS write.
-__device__ __attribute__((always_inline)) void stage_rows(float* xstage, const float* src, int64_t ld, int64_t k0,
-                                                         const Rows8& rows) {
-  const int l = lane_id();
-  float v[16];
+  const int npairs = A.F / kWave;  // pairs of one h row per lane: element l + 64 i
+  while (rows != 0ull) {
+    const int r = (int)__builtin_ctzll(rows);
+    rows &= rows - 1ull;
+    const uint64_t* src = A.h + (int64_t)r * A.F + l;
+    for (int i0 = 0; i0 < npairs; i0 += kMaxP) {
+      float v[kMaxP];
+      poll_pairs<kMaxP>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl, v);
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const float* srow = src + (int64_t)rows.row[r] * ld + k0;
-    v[2 * r] = r < rows.cnt ? ld_dev(srow + l) : 0.0f;
-    v[2 * r + 1] = r < rows.cnt ? ld_dev(srow + 64 + l) : 0.0f;
-  }
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    if (r < rows.cnt) {
-      xstage[r * 128 + l] = v[2 * r];
-      xstage[r * 128 + 64 + l] = v[2 * r + 1];
+      for (int i = 0; i < kMaxP; ++i) {
+        if (i0 + i < npairs) {
+          const int kk = (i0 + i) * kWave + l;
+          C.act[(kk >> 7) * kXPad + (kk & 127)] = v[i];
+        }
+      }
     }
-  }
-  __builtin_amdgcn_wave_barrier();
-}
-
-// Folds the partials of a unit in chunk order; returns acc[r] for the lane's
-// column.  Per row, the chunk partials (and the scales, once) are loaded in
-// one batch, then chained.
-constexpr int kMaxChunks = 16;
-
-__device__ __attribute__((always_inline)) void fold(const float* part, const float* scl, int chunks, int rm, int cnt,
-                                                   bool int8, float (&acc)[8]) {
-  const int l = lane_id();
-  float s[kMaxChunks];
+    __builtin_amdgcn_wave_barrier();
+    const float part = chain<INT8>(st, C.act + g * kXPad);
+    float acc = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) s[c] = (int8 && c < chunks) ? ld_dev(scl + c * 64 + l) : 1.0f;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    acc[r] = 0.0f;
-    if (r < cnt) {
-      float v[kMaxChunks];
-#pragma unroll
-      for (int c = 0; c < kMaxChunks; ++c) v[c] = c < chunks ? ld_dev(part + (c * rm + r) * 64 + l) : 0.0f;
-      float x = 0.0f;
-#pragma unroll
-      for (int c = 0; c < kMaxChunks; ++c)
-        if (c < chunks) x = int8 ? __builtin_fmaf(s[c], v[c], x) : x + v[c];
-      acc[r] = x;
+    for (int gg = 0; gg < kMaxG; ++gg) {
+      if (gg < A.gf) {
+        const float pv = shfl(part, base + gg);
+        if constexpr (INT8)
+          acc = __builtin_fmaf(sv[gg], pv, acc);
+        else
+          acc = acc + pv;
+      }
     }
+    if (g == 0 && l < lanes) st_pair(A.y + (int64_t)r * A.H + n0 + c, acc, C.tag);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
-__device__ __attribute__((always_inline)) void combine_block(const FusedArgs& a, int cb) {
-  const int l = lane_id();
-  const int n = cb * 64 + l;
-  if (n >= a.H) return;
+// 64 columns of the output: sh = shared-down chunk partials added in order;
+// out = fma chain over j of w_j * y_j from 0, plus sh.  The last comb task of
+// the launch advances the launch tag.
+__device__ __attribute__((always_inline)) void task_comb(const FusedArgs& A, const Ctx& C, const Task& k,
+                                                         uint32_t epoch) {
+  constexpr int kMaxG = 16;
   constexpr int kMaxK = 8;
-  for (int t = 0; t < a.B; ++t) {
-    float w[kMaxK], y[kMaxK];
+  const int l = lane();
+  const int n = k.a * 64 + l;
+  for (int t = 0; t < A.B; ++t) {
+    float v[kMaxG];
+    poll_pairs<kMaxG>(A.p_sdn + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag, A.ctl,
+                      v);
+    float shv = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-      const int i = t * a.topk + j;
-      w[j] = j < a.topk ? ld_dev(a.wts + i) : 0.0f;
-      y[j] = j < a.topk ? ld_dev(a.y + (int64_t)i * a.H + n) : 0.0f;
-    }
-    const float shv = ld_dev(a.sh + (int64_t)t * a.H + n);
+    for (int g = 0; g < kMaxG; ++g)
+      if (g < A.gfs) shv = shv + v[g];
+    float y[kMaxK];
+    poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, y);
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxK; ++j)
-      if (j < a.topk) acc = __builtin_fmaf(w[j], y[j], acc);
-    a.out[(int64_t)t * a.H + n] = acc + shv;
+      if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
+    A.out[(int64_t)t * A.H + n] = acc + shv;
+  }
+  uint32_t old = 0;
+  if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = shfl(old, 0);
+  if (old + 1u == (uint32_t)A.cb_h) {
+    uint32_t spin = 0;
+    while (!poll_done(ld_word(A.ctl + C_ARRIVED) >= gridDim.x, spin, A.ctl)) {
+    }
+    if (l == 0) {
+      st_word(A.ctl + C_ARRIVED, 0u);
+      st_word(A.ctl + C_COMBINED, 0u);
+      st_word(A.ctl + C_EPOCH, epoch + 1u);
+    }
   }
 }
 
-__device__ __attribute__((always_inline)) void after_down_fold(const FusedArgs& a, int cb) {
-  const uint32_t target = (uint32_t)ld_dev(a.n_groups) + 1u;
-  if (signal(ctl_out(a) + cb) + 1u == target) combine_block(a, cb);
+// Runs task t.
+__device__ __attribute__((always_inline)) void run_task(const FusedArgs& A, const Ctx& C, const Route& rt, int t,
+                                                        const Task& k, uint32_t epoch) {
+  UOCR_TRACE(A, t, 0);
+  switch (k.kind) {
+    case K_SGU: task_sgu(A, C, k); break;
+    case K_RGU:
+      if (A.int8)
+        task_rgu<true>(A, C, rt, k);
+      else
+        task_rgu<false>(A, C, rt, k);
+      break;
+    case K_SFOLD: task_sfold(A, C, k); break;
+    case K_SDN: task_sdn(A, C, k); break;
+    case K_RDN:
+      if (A.int8)
+        task_rdn<true>(A, C, rt, k);
+      else
+        task_rdn<false>(A, C, rt, k);
+      break;
+    case K_COMB: task_comb(A, C, k, epoch); break;
+    default: break;
+  }
+  UOCR_TRACE(A, t, 2);
+  if (A.trace != nullptr && lane() == 0)
+    A.trace[(int64_t)t * 8 + 7] = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
 }
 
-__device__ __attribute__((always_inline)) void chunk_task(const FusedArgs& a, const Wave& W, const Task& k, int tid) {
-  const int l = lane_id();
-  UOCR_TRACE(a, tid, 0);
-  if (k.kind == T_RGU || k.kind == T_RDN) {
-    wait_ge(a.ctl, C_READY, 1u);
-    if (k.slot >= ld_dev(a.n_groups)) return;
-  }
-  UOCR_TRACE(a, tid, 1);
-  Stage st;
-  issue_task(a, k, st);
-  if (a.trace != nullptr) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    UOCR_TRACE(a, tid, 2);
-  }
-  const Rows8 rows = unit_rows(a, k);
-  const bool routed = k.kind == T_RGU || k.kind == T_RDN;
-  const bool int8 = routed && a.int8;
-  const int subtiles = int8 ? 1 : 2;
-  const bool kblocked = !routed;
-  int e = 0;
-  if (routed) e = ld_dev(a.group_expert + k.slot);
+__global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs A) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int wave = (int)(threadIdx.x >> 6);
+  Ctx C;
+  float* xs = (float*)lds;
+  int* r_ids = (int*)(lds + A.lds_x);
+  float* r_wts = (float*)(lds + A.lds_x + 256);
+  int* r_done = (int*)(lds + A.lds_x + 512);  // tokens routed so far
+  C.xs = xs;
+  C.r_ids = r_ids;
+  C.r_wts = r_wts;
+  C.act = (float*)(lds + A.lds_x + 528 + wave * A.lds_act);
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_word(A.ctl + C_EPOCH));
+  C.tag = epoch + 1u;
 
-  XSrc xs;
-  xs.from_lds = false;
-  xs.lds = W.xstage;
-  int64_t kx0;  // first activation element of the chunk
-  if (k.kind == T_SGU || k.kind == T_RGU) {
-    kx0 = (int64_t)k.c * 128;
-    const int div = k.kind == T_RGU ? a.topk : 1;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) xs.row[r] = uniform_ptr(a.x + (int64_t)(rows.row[r] / div) * a.H + kx0);
-  } else if (k.kind == T_SDN) {
-    wait_ge(a.ctl, C_HS, (uint32_t)a.cb_fs);
-    stage_rows(W.xstage, a.hs, a.Fs, (int64_t)k.c * 128, rows);
-    xs.from_lds = true;
-  } else {
-    wait_ge(a.ctl, C_BASE + a.cb_fs + k.slot, (uint32_t)a.cb_f);
-    stage_rows(W.xstage, a.h, a.F, (int64_t)k.c * 128, rows);
-    xs.from_lds = true;
+  // x rows into LDS, each 128-element chunk padded to kXPad floats
+  for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
+    const int t = i / A.H;
+    const int kk = i - t * A.H;
+    xs[t * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
   }
+  if (threadIdx.x == 0) *r_done = 0;
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(A.ctl + C_ARRIVED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  UOCR_TRACE(a, tid, 3);
-  float part[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) part[r] = 0.0f;
-  if (xs.from_lds)
-    run_chain_rows<true>(rows.cnt, int8, subtiles, W.tile, st, kblocked, xs, part);
-  else
-    run_chain_rows<false>(rows.cnt, int8, subtiles, W.tile, st, kblocked, xs, part);
-
-  // partials (and, for int8, the chunk's scale per column)
-  const int rm = a.B;
-  float* pbase;
-  float* sbase = nullptr;
-  int unit_chunks, pc;
-  uint32_t* counter;
-  if (k.kind == T_SGU) {
-    unit_chunks = 2 * a.ch_h;
-    pc = k.p * a.ch_h + k.c;
-    pbase = a.p_sgu + (int64_t)k.cb * unit_chunks * rm * 64;
-    counter = ctl_sgu(a) + k.cb;
-  } else if (k.kind == T_RGU) {
-    unit_chunks = 2 * a.ch_h;
-    pc = k.p * a.ch_h + k.c;
-    const int unit = k.slot * a.cb_f + k.cb;
-    pbase = a.p_rgu + (int64_t)unit * unit_chunks * rm * 64;
-    sbase = a.s_rgu + (int64_t)unit * unit_chunks * 64;
-    counter = ctl_rgu(a) + unit;
-  } else if (k.kind == T_SDN) {
-    unit_chunks = a.ch_fs;
-    pc = k.c;
-    pbase = a.p_sdn + (int64_t)k.cb * unit_chunks * rm * 64;
-    counter = ctl_sdn(a) + k.cb;
-  } else {
-    unit_chunks = a.ch_f;
-    pc = k.c;
-    const int unit = k.slot * a.cb_h + k.cb;
-    pbase = a.p_rdn + (int64_t)unit * unit_chunks * rm * 64;
-    sbase = a.s_rdn + (int64_t)unit * unit_chunks * 64;
-    counter = ctl_rdn(a) + unit;
+  const int nwaves = (int)gridDim.x * kWaves;
+  int t = wave * (int)gridDim.x + (int)blockIdx.x;
+  for (; t < A.E; t += nwaves) {
+    UOCR_TRACE(A, t, 0);
+    router_task(A, C, t);
+    UOCR_TRACE(A, t, 2);
+    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = wave * (int)gridDim.x + (int)blockIdx.x;
   }
-#pragma unroll
-  for (int r = 0; r < 8; ++r)
-    if (r < rows.cnt) st_dev(pbase + (pc * rm + r) * 64 + l, part[r]);
-  const int N = (k.kind == T_SGU) ? a.Fs : (k.kind == T_RGU ? a.F : a.H);
-  const int n = min(k.cb * 64 + l, N - 1);
-  if (int8) {
-    const float* scales = k.kind == T_RGU ? (k.p == 0 ? a.gate_s : a.up_s) : a.down_s;
-    const int groups = k.kind == T_RGU ? a.ch_h : a.ch_f;
-    st_dev(sbase + pc * 64 + l, ldg(scales + ((int64_t)e * N + n) * groups + k.c));
+  // The first task after the router tasks may be a shared gate/up chunk,
+  // which does not need the routing: it runs now, its weights loading while
+  // the routing waves poll the logits.  The routing of token i is computed by
+  // wave kWaves-1-i (high waves rarely hold such a chunk).
+  const int rwave = kWaves - 1 - wave;
+  if (t < A.E + A.n_sgu) {
+    Stage<false> st;
+    const Task k = task_at(A, 0, t);
+    UOCR_TRACE(A, t, 0);
+    issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
+    if (rwave < A.B) route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
+    sgu_rows(A, C, k, st);
+    UOCR_TRACE(A, t, 2);
+    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = wave * (int)gridDim.x + (int)blockIdx.x;
+    t += nwaves;
+  } else if (rwave < A.B) {
+    route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
   }
-  UOCR_TRACE(a, tid, 4);
-  const bool last = signal(counter) + 1u == (uint32_t)unit_chunks;
-  UOCR_TRACE(a, tid, 5);
-  if (!last) return;
-
-  // ---- the last chunk of the unit: fold
-  const bool valid = k.cb * 64 + l < N;
-  float acc[8];
-  if (k.kind == T_SGU || k.kind == T_RGU) {
-    float accu[8];
-    const int half = a.ch_h;
-    fold(pbase, sbase, half, rm, rows.cnt, int8, acc);
-    fold(pbase + (int64_t)half * rm * 64, sbase ? sbase + half * 64 : nullptr, half, rm, rows.cnt, int8, accu);
-    float* dst = k.kind == T_SGU ? a.hs : a.h;
-    const int ldd = k.kind == T_SGU ? a.Fs : a.F;
-    if (valid) {
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-        if (r < rows.cnt) st_dev(dst + (int64_t)rows.row[r] * ldd + n, silu(acc[r]) * accu[r]);
+  {
+    uint32_t spin = 0;
+    while (!poll_done(__hip_atomic_load(r_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= A.B, spin,
+                      A.ctl)) {
     }
-    if (k.kind == T_SGU)
-      signal(a.ctl + C_HS);
-    else
-      signal(ctl_hready(a) + k.slot);
-  } else {
-    fold(pbase, sbase, unit_chunks, rm, rows.cnt, int8, acc);
-    float* dst = k.kind == T_SDN ? a.sh : a.y;
-    if (valid) {
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-        if (r < rows.cnt) st_dev(dst + (int64_t)rows.row[r] * a.H + n, acc[r]);
-    }
-    after_down_fold(a, k.cb);
+    asm volatile("" ::: "memory");
   }
-  UOCR_TRACE(a, tid, 6);
-}
-
-__global__ void __launch_bounds__(kWavesPerWg * 64) k_decode_fused(FusedArgs a) {
-  extern __shared__ char lds[];
-  const int wv = (int)(threadIdx.x >> 6);
-  Wave W;
-  W.tile = lds + wv * (kTileBytes + padded_rows(a.B) * 128 * 4);
-  W.xstage = (float*)(W.tile + kTileBytes);
-  const int nwaves = (int)gridDim.x * kWavesPerWg;
-  int t = (int)blockIdx.x * kWavesPerWg + wv;
-
-  for (; t < a.n_tasks; t += nwaves) {
-    const Task k = decode_task(a, t);
-    if (k.kind == T_ROUTER) {
-      UOCR_TRACE(a, t, 0);
-      router_task(a, k.e);
-      UOCR_TRACE(a, t, 3);
-      if (signal(a.ctl + C_ROUTER) + 1u == (uint32_t)a.n_router) {
-        UOCR_TRACE(a, t, 5);
-        routing(a);
-        signal(a.ctl + C_READY);
-        UOCR_TRACE(a, t, 6);
-      }
-    } else if (k.kind != T_NONE) {
-      chunk_task(a, W, k, t);
-    }
-    if (a.trace != nullptr && lane_id() == 0) a.trace[(int64_t)t * 8 + 7] = (int64_t)((int)blockIdx.x * kWavesPerWg + wv);
-  }
-
-  // the last wave of the launch resets the control words for the next one
-  if (signal(a.ctl + C_DONE) + 1u == (uint32_t)nwaves) {
-    const int words = a.ctl_words;
-    for (int i = lane_id(); i < words; i += kWave)
-      if (i != C_DONE && i != C_ERR) st_dev(a.ctl + i, 0u);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (lane_id() == 0) st_dev(a.ctl + C_DONE, 0u);
-  }
+  const Route rt = make_route(A, r_ids);
+  const int n_tasks = task_count(A, rt.ng);
+  for (; t < n_tasks; t += nwaves) run_task(A, C, rt, t, task_at(A, rt.ng, t), epoch);
 }
 
 }  // namespace
 
-int fused_ctl_words(int cb_fs, int cb_h, int cb_f, int max_slots) {
-  return C_BASE + cb_fs + 64 + cb_h + cb_h + max_slots * cb_f + max_slots * cb_h;
+FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
+  FusedLayout L{};
+  L.gh = H / 128;
+  L.gf = F / 128;
+  L.gfs = Fs / 128;
+  L.c_gu = L.gh > 0 ? 64 / (2 * L.gh) : 0;
+  L.c_dn = L.gf > 0 ? 64 / L.gf : 0;
+  L.per_e_gu = L.c_gu > 0 ? (F + L.c_gu - 1) / L.c_gu : 0;
+  L.per_e_dn = L.c_dn > 0 ? (H + L.c_dn - 1) / L.c_dn : 0;
+  L.cb_fs = Fs / 64;
+  L.cb_h = H / 64;
+  L.n_sgu = L.cb_fs * 2 * L.gh;
+  L.n_sdn = L.cb_h * L.gfs;
+  L.lds_x = B * L.gh * kXPad * 4;
+  const int act_rows = B * 128 * 4;
+  const int act_h = L.gf * kXPad * 4;
+  L.lds_act = act_rows > act_h ? act_rows : act_h;
+  L.lds_bytes = (size_t)L.lds_x + 528 + (size_t)kWaves * L.lds_act;
+  const int R = B * topk;
+  const int slots = E < R ? E : R;
+  L.max_tasks = E + L.n_sgu + slots * L.per_e_gu + L.cb_fs + L.n_sdn + slots * L.per_e_dn + L.cb_h;
+  // tagged words for the largest batch (8 tokens) of this layer
+  const int64_t rmax = 8 * (int64_t)topk;
+  L.off_logits = 0;
+  L.off_h = L.off_logits + 8 * 64;
+  L.off_y = L.off_h + rmax * F;
+  L.off_hs = L.off_y + rmax * H;
+  L.off_psgu = L.off_hs + 8 * (int64_t)Fs;
+  L.off_psdn = L.off_psgu + (int64_t)L.cb_fs * 2 * L.gh * 8 * 64;
+  L.data_words = L.off_psdn + (int64_t)L.cb_h * L.gfs * 8 * 64;
+  return L;
 }
 
-size_t fused_lds_bytes(int B) { return (size_t)kWavesPerWg * (kTileBytes + padded_rows(B) * 128 * 4); }
-
-hipError_t fused_grid(int B, int* grid) {
+hipError_t fused_grid(size_t lds_bytes, int* grid) {
   int dev = 0, cus = 0, per_cu = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e == hipSuccess)
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_fused, kWavesPerWg * 64, fused_lds_bytes(B));
+    e = hipFuncSetAttribute((const void*)k_decode_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_fused, kThreads, lds_bytes);
   if (e != hipSuccess) return e;
-  *grid = cus * (per_cu < 1 ? 1 : per_cu);
+  *grid = cus * per_cu;
   return hipSuccess;
 }
 
-hipError_t launch_decode_fused(const FusedArgs& a, int grid, hipStream_t s) {
-  UOCR_LAUNCH("decode_fused", k_decode_fused, dim3(grid), dim3(kWavesPerWg * 64), fused_lds_bytes(a.B), s, a);
+hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+  UOCR_LAUNCH("decode_fused", k_decode_fused, dim3(grid), dim3(kThreads), lds_bytes, s, a);
   return hipGetLastError();
 }
 
-__global__ void k_zero_words(uint32_t* p, int n) {
-  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+__global__ void k_zero_words(uint32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
 }
 
-hipError_t launch_zero_words(uint32_t* p, int n, hipStream_t s) {
+hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  UOCR_LAUNCH("zero_words", k_zero_words, dim3((n + 255) / 256), dim3(256), 0, s, p, n);
+  UOCR_LAUNCH("zero_words", k_zero_words, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
   return hipGetLastError();
 }
 

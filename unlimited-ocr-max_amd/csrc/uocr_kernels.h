@@ -137,6 +137,24 @@ hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared
 
 // ---- the persistent decode layer (decode.hip) ----
 
+constexpr int kFusedWaves = 16;  // waves per workgroup, one workgroup per CU
+constexpr int kFusedXPad = 132;  // floats per 128-element chunk of an LDS activation row
+
+// Task layout, LDS and tagged-buffer sizes of one layer shape.
+struct FusedLayout {
+  int gh, gf, gfs;          // 128-element chunks of H, F, Fs
+  int c_gu, c_dn;           // columns per routed gate/up and down task
+  int per_e_gu, per_e_dn;   // routed tasks per selected expert
+  int cb_fs, cb_h;          // 64-column blocks of Fs and H
+  int n_sgu, n_sdn;         // shared chunk tasks
+  int lds_x, lds_act;       // LDS bytes: x rows, per-wave activation stage
+  size_t lds_bytes;
+  int max_tasks;
+  // offsets (in 64-bit words) of the tagged buffers, sized for 8 tokens
+  int64_t off_logits, off_h, off_y, off_hs, off_psgu, off_psdn, data_words;
+};
+FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk);
+
 struct FusedArgs {
   int B, E, H, F, Fs, topk;
   int int8, renorm;
@@ -152,39 +170,24 @@ struct FusedArgs {
   const uint16_t* sh_down;
   const float* x;
   float* out;
-  // control words (library-owned, zero between launches)
+  int32_t* ids_out;  // optional routing outputs [B*topk]
+  float* wts_out;
+  // library-owned, zeroed when allocated: control words and tagged pairs
   uint32_t* ctl;
-  int ctl_words;
-  // workspace
-  float* logits;  // [B][64]
-  int* ids;       // [B*topk]
-  float* wts;     // [B*topk]
-  int* n_groups;
-  int* group_expert;  // [64]
-  int* group_start;   // [65]
-  int* group_rows;    // [64]
-  float* p_sgu;
-  float* p_rgu;
-  float* s_rgu;
-  float* p_sdn;
-  float* p_rdn;
-  float* s_rdn;
-  float* hs;  // [B][Fs]
-  float* h;   // [B*topk][F]
-  float* sh;  // [B][H]
-  float* y;   // [B*topk][H]
-  // task layout
-  int cb_f, cb_fs, cb_h;  // 64-column blocks of F, Fs, H
-  int ch_h, ch_f, ch_fs;  // 128-element chunks of H, F, Fs
-  int max_slots;
-  int n_router, n_sgu, n_rgu, n_sdn, n_rdn, n_tasks;
+  uint64_t* logits;  // [B][64]
+  uint64_t* h;       // [B*topk][F]
+  uint64_t* y;       // [B*topk][H]
+  uint64_t* hs;      // [B][Fs]
+  uint64_t* p_sgu;   // [Fs/64][2][H/128][B][64]
+  uint64_t* p_sdn;   // [H/64][Fs/128][B][64]
+  // layout (FusedLayout)
+  int gh, gf, gfs, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, lds_x, lds_act;
+  float inv_gh, inv_gf;
   // optional per-task phase timestamps (8 words per task), null when off
   int64_t* trace;
 };
-int fused_ctl_words(int cb_fs, int cb_h, int cb_f, int max_slots);
-size_t fused_lds_bytes(int B);
-hipError_t fused_grid(int B, int* grid);
-hipError_t launch_decode_fused(const FusedArgs& a, int grid, hipStream_t s);
-hipError_t launch_zero_words(uint32_t* p, int n, hipStream_t s);
+hipError_t fused_grid(size_t lds_bytes, int* grid);
+hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s);
+hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t s);
 
 }  // namespace uocr

@@ -115,67 +115,104 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
   return hipSuccess;
 }
 
-// Control words of the persistent decode kernel: a per-device arena of
-// kCtlSlots slots, allocated and zeroed by the first call on the device (which
-// must not be under stream capture); each stream takes a slot when first seen
-// (round robin), so no allocation happens later, under capture included.
-// Every launch leaves its slot zero again.  Launches on streams that share a
-// slot must not overlap in time.
-constexpr int kCtlWords = 1 << 14;
-constexpr int kCtlSlots = 16;
-struct CtlArena {
-  uint32_t* base = nullptr;
+// State of the persistent decode kernel: per device, kFusedSlots slots of
+// control words and tagged buffers, allocated and zeroed by the first call on
+// the device (which must not be under stream capture, and neither may a later
+// call whose layer needs more room); each stream takes a slot when first seen
+// (round robin), so streams first seen under capture need no allocation.
+// Launches on streams that share a slot must not overlap in time.
+constexpr int kFusedCtlWords = 64;
+constexpr int kFusedSlots = 16;
+struct FusedSlot {
+  uint32_t* ctl = nullptr;
+  uint64_t* data = nullptr;
+};
+struct FusedDevice {
+  uint32_t* ctl = nullptr;   // kFusedSlots x kFusedCtlWords
+  uint64_t* data = nullptr;  // kFusedSlots x words
+  int64_t words = 0;
   int next = 0;
   std::map<hipStream_t, int> slot;
 };
-std::map<int, CtlArena> g_ctl;
-
-hipError_t ctl_words(hipStream_t stream, uint32_t** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  CtlArena& a = g_ctl[dev];
-  if (a.base == nullptr) {
-    e = hipMalloc(&a.base, (size_t)kCtlSlots * kCtlWords * sizeof(uint32_t));
-    if (e != hipSuccess) {
-      a.base = nullptr;
-      return e;
-    }
-    e = launch_zero_words(a.base, kCtlSlots * kCtlWords, stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    if (e != hipSuccess) return e;
-  }
-  auto it = a.slot.find(stream);
-  int k;
-  if (it == a.slot.end()) {
-    k = a.next++ % kCtlSlots;
-    a.slot[stream] = k;
-  } else {
-    k = it->second;
-  }
-  *out = a.base + (size_t)k * kCtlWords;
-  return hipSuccess;
-}
-
-std::map<std::pair<int, int>, int> g_fused_grid;  // (device, B) -> workgroups
+std::map<int, FusedDevice> g_fused;
+std::map<std::pair<int, size_t>, int> g_fused_grid;  // (device, LDS bytes) -> workgroups
 
 // Optional phase trace of the next persistent decode launch (diagnostics).
 int64_t* g_trace = nullptr;
 int64_t g_trace_words = 0;
+int g_trace_grid = 0;
 
-hipError_t fused_grid_cached(int B, int* grid) {
+bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// The slot of (current device, stream) with room for `data_words` tagged
+// words; *need_alloc is set when that needs an allocation under capture.
+hipError_t fused_slot(hipStream_t stream, int64_t data_words, FusedSlot* out, bool* need_alloc) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  auto it = g_fused_grid.find({dev, B});
+  FusedDevice& d = g_fused[dev];
+  *need_alloc = false;
+  if (d.ctl == nullptr || d.words < data_words) {
+    if (capturing(stream)) {
+      *need_alloc = true;
+      return hipSuccess;
+    }
+    e = hipDeviceSynchronize();  // queued launches may still use the old buffers
+    if (e != hipSuccess) return e;
+    if (d.ctl == nullptr) {
+      e = hipMalloc(&d.ctl, (size_t)kFusedSlots * kFusedCtlWords * sizeof(uint32_t));
+      if (e != hipSuccess) {
+        d.ctl = nullptr;
+        return e;
+      }
+      e = launch_zero_words(d.ctl, (int64_t)kFusedSlots * kFusedCtlWords, stream);
+      if (e != hipSuccess) return e;
+    }
+    if (d.words < data_words) {
+      if (d.data != nullptr) (void)hipFree(d.data);
+      d.data = nullptr;
+      d.words = 0;
+      e = hipMalloc(&d.data, (size_t)kFusedSlots * data_words * sizeof(uint64_t));
+      if (e != hipSuccess) {
+        d.data = nullptr;
+        return e;
+      }
+      e = launch_zero_words(reinterpret_cast<uint32_t*>(d.data), 2 * kFusedSlots * data_words, stream);
+      if (e != hipSuccess) return e;
+      d.words = data_words;
+    }
+    e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return e;
+  }
+  int k;
+  auto it = d.slot.find(stream);
+  if (it == d.slot.end()) {
+    k = d.next++ % kFusedSlots;
+    d.slot[stream] = k;
+  } else {
+    k = it->second;
+  }
+  out->ctl = d.ctl + (size_t)k * kFusedCtlWords;
+  out->data = d.data + (size_t)k * d.words;
+  return hipSuccess;
+}
+
+hipError_t fused_grid_cached(size_t lds_bytes, int* grid) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  auto it = g_fused_grid.find({dev, lds_bytes});
   if (it != g_fused_grid.end()) {
     *grid = it->second;
     return hipSuccess;
   }
-  e = fused_grid(B, grid);
-  if (e == hipSuccess) g_fused_grid[{dev, B}] = *grid;
+  e = fused_grid(lds_bytes, grid);
+  if (e == hipSuccess) g_fused_grid[{dev, lds_bytes}] = *grid;
   return e;
 }
 
@@ -393,57 +430,66 @@ static DecodeBufs carve_decode(Carve& c, const uocr_moe_layer* L, int64_t B) {
   return d;
 }
 
+// LDS per workgroup on gfx950.
+constexpr size_t kMaxLds = 160 * 1024;
+
 static bool fused_eligible(const uocr_moe_layer* L, int64_t B) {
   const char* env = std::getenv("UOCR_MOE_DECODE");
   if (env != nullptr && std::strcmp(env, "multi") == 0) return false;
-  if (B < 1 || B > 8 || B * L->top_k > 64 || L->num_experts > 64) return false;
-  if (L->hidden % 128 || L->ffn % 128 || L->shared_ffn % 128) return false;
+  if (B < 1 || B > 8 || L->top_k > 8 || B * L->top_k > 64 || L->num_experts > 64) return false;
+  for (int64_t d : {L->hidden, L->ffn, L->shared_ffn})
+    if (d % 128 || d > 2048) return false;
   if (L->int8 && L->group != 128) return false;
-  return true;
+  for (const void* p : {L->gate_proj, L->up_proj, L->down_proj, (const void*)L->shared_gate,
+                        (const void*)L->shared_up, (const void*)L->shared_down})
+    if (!aligned16(p)) return false;
+  const FusedLayout lay = fused_layout((int)B, (int)L->num_experts, (int)L->hidden, (int)L->ffn,
+                                       (int)L->shared_ffn, (int)L->top_k);
+  return lay.lds_bytes <= kMaxLds;
 }
 
-static FusedArgs carve_fused(Carve& c, const uocr_moe_layer* L, int64_t B) {
+static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayout& lay, const FusedSlot& f) {
   FusedArgs a{};
-  const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
-  const int topk = (int)L->top_k;
-  const int R = (int)B * topk;
   a.B = (int)B;
-  a.E = E;
-  a.H = H;
-  a.F = F;
-  a.Fs = Fs;
-  a.topk = topk;
-  a.cb_f = F / 64;
-  a.cb_fs = Fs / 64;
-  a.cb_h = H / 64;
-  a.ch_h = H / 128;
-  a.ch_f = F / 128;
-  a.ch_fs = Fs / 128;
-  a.max_slots = E < R ? E : R;
-  a.n_router = E;
-  a.n_sgu = a.cb_fs * 2 * a.ch_h;
-  a.n_rgu = a.max_slots * a.cb_f * 2 * a.ch_h;
-  a.n_sdn = a.cb_h * a.ch_fs;
-  a.n_rdn = a.max_slots * a.cb_h * a.ch_f;
-  a.n_tasks = a.n_router + a.n_sgu + a.n_rgu + a.n_sdn + a.n_rdn;
-  a.ctl_words = fused_ctl_words(a.cb_fs, a.cb_h, a.cb_f, a.max_slots);
-  a.logits = c.take<float>(B * 64);
-  a.ids = c.take<int>(R);
-  a.wts = c.take<float>(R);
-  a.n_groups = c.take<int>(1);
-  a.group_expert = c.take<int>(64);
-  a.group_start = c.take<int>(65);
-  a.group_rows = c.take<int>(64);
-  a.p_sgu = c.take<float>((size_t)a.cb_fs * 2 * a.ch_h * B * 64);
-  a.p_rgu = c.take<float>((size_t)a.max_slots * a.cb_f * 2 * a.ch_h * B * 64);
-  a.s_rgu = c.take<float>((size_t)a.max_slots * a.cb_f * 2 * a.ch_h * 64);
-  a.p_sdn = c.take<float>((size_t)a.cb_h * a.ch_fs * B * 64);
-  a.p_rdn = c.take<float>((size_t)a.max_slots * a.cb_h * a.ch_f * B * 64);
-  a.s_rdn = c.take<float>((size_t)a.max_slots * a.cb_h * a.ch_f * 64);
-  a.hs = c.take<float>(B * Fs);
-  a.h = c.take<float>((size_t)R * F);
-  a.sh = c.take<float>(B * H);
-  a.y = c.take<float>((size_t)R * H);
+  a.E = (int)L->num_experts;
+  a.H = (int)L->hidden;
+  a.F = (int)L->ffn;
+  a.Fs = (int)L->shared_ffn;
+  a.topk = (int)L->top_k;
+  a.int8 = L->int8;
+  a.renorm = L->renormalize;
+  a.router = L->router;
+  a.gate_w = L->gate_proj;
+  a.up_w = L->up_proj;
+  a.down_w = L->down_proj;
+  a.gate_s = L->gate_proj_scales;
+  a.up_s = L->up_proj_scales;
+  a.down_s = L->down_proj_scales;
+  a.sh_gate = L->shared_gate;
+  a.sh_up = L->shared_up;
+  a.sh_down = L->shared_down;
+  a.ctl = f.ctl;
+  a.logits = f.data + lay.off_logits;
+  a.h = f.data + lay.off_h;
+  a.y = f.data + lay.off_y;
+  a.hs = f.data + lay.off_hs;
+  a.p_sgu = f.data + lay.off_psgu;
+  a.p_sdn = f.data + lay.off_psdn;
+  a.gh = lay.gh;
+  a.gf = lay.gf;
+  a.gfs = lay.gfs;
+  a.c_gu = lay.c_gu;
+  a.c_dn = lay.c_dn;
+  a.per_e_gu = lay.per_e_gu;
+  a.per_e_dn = lay.per_e_dn;
+  a.cb_fs = lay.cb_fs;
+  a.cb_h = lay.cb_h;
+  a.n_sgu = lay.n_sgu;
+  a.n_sdn = lay.n_sdn;
+  a.lds_x = lay.lds_x;
+  a.lds_act = lay.lds_act;
+  a.inv_gh = 1.0f / (float)lay.gh;
+  a.inv_gf = 1.0f / (float)lay.gf;
   return a;
 }
 
@@ -479,11 +525,6 @@ size_t uocr_moe_workspace_bytes(const uocr_moe_layer* layer, int64_t rows, int p
     carve_prefill(c, layer, rows);
   } else {
     carve_decode(c, layer, rows);
-    if (fused_eligible(layer, rows)) {
-      Carve f(nullptr);
-      carve_fused(f, layer, rows);
-      if (f.off > c.off) c.off = f.off;
-    }
   }
   return c.off + 256;
 }
@@ -519,43 +560,34 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
   const hipStream_t s = (hipStream_t)stream;
   const int64_t B = rows, R = rows * L->top_k;
   if (fused_eligible(L, B)) {
-    Carve dry(nullptr);
-    carve_fused(dry, L, B);
-    void* ws = nullptr;
-    if (resolve_workspace(op, workspace, workspace_bytes, dry.off, s, &ws, err, errlen)) return 1;
-    Carve c(ws);
-    FusedArgs a = carve_fused(c, L, B);
-    if (a.ctl_words > kCtlWords) return fail(err, errlen, "%s: the layer needs too many control words", op);
-    hipError_t e = ctl_words(s, &a.ctl);
+    const FusedLayout lay = fused_layout((int)B, (int)L->num_experts, (int)L->hidden, (int)L->ffn,
+                                         (int)L->shared_ffn, (int)L->top_k);
+    FusedSlot slot;
+    bool need_alloc = false;
+    hipError_t e = fused_slot(s, lay.data_words, &slot, &need_alloc);
+    if (e == hipSuccess && need_alloc)
+      return fail(err, errlen,
+                  "%s: the first decode call on a device (or the first with a larger layer) must not be under "
+                  "stream capture",
+                  op);
     int grid = 0;
-    if (e == hipSuccess) e = fused_grid_cached((int)B, &grid);
+    if (e == hipSuccess) e = fused_grid_cached(lay.lds_bytes, &grid);
     if (e != hipSuccess) return hip_fail(err, errlen, op, e);
-    a.int8 = L->int8;
-    a.renorm = L->renormalize;
-    a.router = L->router;
-    a.gate_w = L->gate_proj;
-    a.up_w = L->up_proj;
-    a.down_w = L->down_proj;
-    a.gate_s = L->gate_proj_scales;
-    a.up_s = L->up_proj_scales;
-    a.down_s = L->down_proj_scales;
-    a.sh_gate = L->shared_gate;
-    a.sh_up = L->shared_up;
-    a.sh_down = L->shared_down;
+    if (grid < 1) return fail(err, errlen, "%s: the persistent decode kernel does not fit a CU", op);
+    FusedArgs a = fused_args(L, B, lay, slot);
     a.x = x;
     a.out = out;
+    a.ids_out = expert_ids;
+    a.wts_out = expert_weights;
     {
       std::lock_guard<std::mutex> lock(g_ws_mu);
-      if (g_trace != nullptr && g_trace_words >= (int64_t)a.n_tasks * 8) {
+      if (g_trace != nullptr && g_trace_words >= (int64_t)lay.max_tasks * 8) {
         a.trace = g_trace;
         g_trace = nullptr;
+        g_trace_grid = grid;
       }
     }
-    e = launch_decode_fused(a, grid, s);
-    if (e == hipSuccess && expert_ids)
-      e = hipMemcpyAsync(expert_ids, a.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
-    if (e == hipSuccess && expert_weights)
-      e = hipMemcpyAsync(expert_weights, a.wts, R * sizeof(float), hipMemcpyDeviceToDevice, s);
+    e = launch_decode_fused(a, grid, lay.lds_bytes, s);
     return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
   }
   Carve dry(nullptr);
@@ -797,24 +829,30 @@ int uocr_moe_timing_end(int capacity, float* ms, char* names, size_t name_stride
 }
 
 int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err, size_t errlen) {
+  (void)err;
+  (void)errlen;
   std::lock_guard<std::mutex> lock(g_ws_mu);
+  if (grid_waves) *grid_waves = g_trace_grid * kFusedWaves;
   g_trace = static_cast<int64_t*>(buffer);
   g_trace_words = words;
-  if (grid_waves) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    *grid_waves = 0;
-    for (auto& kv : g_fused_grid)
-      if (kv.first.first == dev) *grid_waves = kv.second * 4;
-  }
   return 0;
 }
 
 int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
   uint32_t* ctl = nullptr;
-  hipError_t e = ctl_words((hipStream_t)stream, &ctl);
+  if (e == hipSuccess) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_fused.find(dev);
+    if (it != g_fused.end() && it->second.ctl != nullptr) {
+      auto sl = it->second.slot.find((hipStream_t)stream);
+      if (sl != it->second.slot.end()) ctl = it->second.ctl + (size_t)sl->second * kFusedCtlWords;
+    }
+  }
   uint32_t v = 0;
-  if (e == hipSuccess) e = hipMemcpyAsync(&v, ctl + 4, sizeof(v), hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess && ctl != nullptr)
+    e = hipMemcpyAsync(&v, ctl + 4, sizeof(v), hipMemcpyDeviceToHost, (hipStream_t)stream);
   if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(err, errlen, "uocr_moe_fused_errors", e);
   if (errors) *errors = v;
@@ -826,9 +864,12 @@ void uocr_moe_release(void) {
   for (auto& kv : g_ws)
     if (kv.second.ptr != nullptr) (void)hipFree(kv.second.ptr);
   g_ws.clear();
-  for (auto& kv : g_ctl)
-    if (kv.second.base != nullptr) (void)hipFree(kv.second.base);
-  g_ctl.clear();
+  for (auto& kv : g_fused) {
+    if (kv.second.ctl != nullptr) (void)hipFree(kv.second.ctl);
+    if (kv.second.data != nullptr) (void)hipFree(kv.second.data);
+  }
+  g_fused.clear();
+  g_fused_grid.clear();
 }
 
 }  // extern "C"
