@@ -103,12 +103,6 @@ def decode_bytes(u: int, rows: int, int8: bool) -> int:
     return u * expert_bytes(int8) + 3 * FS * H * 2 + E * H * 4 + 2 * rows * H * 4
 
 
-def gateup_bytes(u: int, rows: int, int8: bool) -> int:
-    """The fused gate/up launch: routed gate+up weights, shared gate+up weights, x in, h out."""
-    routed = 2 * F * H + 4 * 2 * F * (H // GROUP) if int8 else 2 * F * H * 2
-    return u * routed + 2 * FS * H * 2 + rows * H * 4 + (rows * TOPK * F + rows * FS) * 4
-
-
 def prefill_flops(T: int) -> float:
     return 2.0 * T * TOPK * 3 * F * H + 2.0 * T * 3 * FS * H + 2.0 * T * H * E
 
@@ -198,8 +192,8 @@ def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: st
     warm_gbs = decode_bytes(u_of[0], B, int8) / (warm_us * 1e-6) / 1e9
     # live per-kernel durations over one rotation (eager; events around each launch)
     kt = kernel_times([lambda l=l, p=p: layers[l].decode_rows(pool[p], workspace=ws) for l, p in plan[: 4 * LAYERS]])
-    gu = kt.get("gemv_gateup", [])
-    gu_bytes = [gateup_bytes(u_of[p], B, int8) for _, p in plan[: len(gu)]]
+    fused = kt.get("decode_fused", [])
+    fused_bytes = [decode_bytes(u_of[p], B, int8) for _, p in plan[: len(fused)]]
     res = {
         "us_per_layer": round(us, 3),
         "tokens_per_s": round(B / (us * 1e-6), 1),
@@ -212,12 +206,12 @@ def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: st
         "kernels_us_avg": {k: round(1e3 * statistics.mean(v), 3) for k, v in kt.items()},
         "kernel_sum_us_avg": round(1e3 * sum(sum(v) for v in kt.values()) / (4 * LAYERS), 3),
     }
-    if gu:
-        res["gateup_kernel"] = {
-            "launches": len(gu),
-            "avg_us": round(1e3 * statistics.mean(gu), 3),
-            "avg_bytes": int(statistics.mean(gu_bytes)),
-            "gbs": round(sum(gu_bytes) / (sum(gu) * 1e-3) / 1e9, 1),
+    if fused:
+        res["fused_kernel"] = {
+            "launches": len(fused),
+            "avg_us": round(1e3 * statistics.mean(fused), 3),
+            "avg_bytes": int(statistics.mean(fused_bytes)),
+            "gbs": round(sum(fused_bytes) / (sum(fused) * 1e-3) / 1e9, 1),
         }
     return res
 
@@ -381,7 +375,7 @@ def main() -> int:
         del bf
 
     b1 = results["decode_int8_b1"]
-    gu = b1.get("gateup_kernel", {})
+    fk = b1.get("fused_kernel", {})
     line = {
         "metric": METRIC,
         "value": b1["us_per_layer"],
@@ -400,14 +394,14 @@ def main() -> int:
                    "group": GROUP, "batch": 1, "layers_rotated": LAYERS},
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_gateup (routed int8 gate+up, shared gate+up, SwiGLU), decode B=1",
-            "achieved": gu.get("gbs"),
+            "kernel": "decode_fused (the whole int8 MoE layer in one persistent kernel), decode B=1",
+            "achieved": fk.get("gbs"),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gu["gbs"] / HBM_PEAK_GBS, 4) if gu else None,
+            "frac": round(fk["gbs"] / HBM_PEAK_GBS, 4) if fk else None,
             "traffic": None,
-            "algorithmic_bytes_per_launch": gu.get("avg_bytes"),
-            "avg_launch_us": gu.get("avg_us"),
+            "algorithmic_bytes_per_launch": fk.get("avg_bytes"),
+            "avg_launch_us": fk.get("avg_us"),
         },
         "cpu_baseline": None if cpu is None else {
             "value": cpu["b1_us"], "unit": "us", "cores": cpu["cores"], "kind": "port",

@@ -8,7 +8,7 @@
 // 128-element chunk added in chunk order; SwiGLU; the routing-weighted fma
 // combine plus the shared experts.
 //
-// Work decomposition.  One workgroup of 16 waves per CU; the layer is a list of
+// Work decomposition.  One workgroup of 12 waves per CU; the layer is a list of
 // tasks dealt round robin to the waves (task t to the wave of rank t mod
 // waves, ranks interleaved across workgroups so neighbouring tasks land on
 // different CUs and XCDs), every wave walking its tasks in increasing order:
@@ -26,7 +26,7 @@
 // inside the wave (lane shuffles); only the shared experts, whose chunks are
 // spread over tasks, fold partials written by other waves.  Each lane loads
 // the weights of its own row and chunk (128 int8 or 256 bf16 bytes, 16 bytes
-// per load) straight into registers; 16 waves per CU keep enough loads in
+// per load) straight into registers; 12 waves per CU keep enough loads in
 // flight without a software pipeline.
 //
 // Synchronisation.  Every value one wave hands to another (logits, partials,
@@ -58,6 +58,17 @@ constexpr uint32_t kSpinLimit = 1u << 16;  // polls per wait (tens of ms): real 
 // control words
 constexpr int C_EPOCH = 0, C_ARRIVED = 1, C_COMBINED = 2, C_ERR = 4;
 
+// The logits are written to kLogitCopies copies; workgroup b polls copy
+// b % kLogitCopies, so no single memory channel serves every poller.
+constexpr int kLogitCopies = kFusedLogitCopies;
+constexpr int kLogitCopyWords = kFusedLogitCopyWords;
+
+// Kernel arguments are read through a constant-address-space reference
+// (scalar loads); the task loop re-derives the pointer every iteration so
+// that the compiler reloads fields where they are used instead of keeping
+// every field in scalar registers across the loop.
+#define KA __attribute__((address_space(4)))
+
 // Lane index through a volatile asm: recomputed where it is used, so that the
 // compiler does not hoist lane-derived values (shuffle addresses, masks) out
 // of the task loop and keep them live across every task.
@@ -78,16 +89,57 @@ __device__ __forceinline__ uint64_t shfl(uint64_t v, int src) {
   return ((uint64_t)shfl((uint32_t)(v >> 32), src) << 32) | shfl((uint32_t)v, src);
 }
 
-// Halving-tree sum over the 64 lanes, v[l] += v[l + off] for off = 32..1;
-// lane 0 ends with the total (lanes past the wave read their own value, which
-// is never used).
+// v of lane l + OFF for lanes l < OFF (OFF = 32, 16, 8, 4, 2, 1; other
+// lanes get values that are never used): v_permlane32/16_swap for the two
+// halving steps across 16-lane rows, DPP row_shl inside a row.  No LDS round
+// trip.
+template <int OFF>
+__device__ __forceinline__ uint32_t from_up(uint32_t v) {
+  if constexpr (OFF == 32) return __builtin_amdgcn_permlane32_swap(v, v, false, false)[1];
+  else if constexpr (OFF == 16) return __builtin_amdgcn_permlane16_swap(v, v, false, false)[1];
+  else return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + OFF, 0xf, 0xf, false);
+}
+template <int OFF>
+__device__ __forceinline__ float from_up(float v) { return __uint_as_float(from_up<OFF>(__float_as_uint(v))); }
+
+// Halving-tree sum over the 64 lanes, v[l] += v[l + off] for off = 32..1,
+// broadcast from lane 0 (the same additions, in the same order, as
+// wave_tree_sum in uocr_device.h).
 __device__ __forceinline__ float tree_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const int l = lane();
-    v = v + shfl(v, l + off < kWave ? l + off : l);
-  }
-  return v;
+  v = v + from_up<32>(v);
+  v = v + from_up<16>(v);
+  v = v + from_up<8>(v);
+  v = v + from_up<4>(v);
+  v = v + from_up<2>(v);
+  v = v + from_up<1>(v);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ float tree_max(float v) {
+  v = fmaxf(v, from_up<32>(v));
+  v = fmaxf(v, from_up<16>(v));
+  v = fmaxf(v, from_up<8>(v));
+  v = fmaxf(v, from_up<4>(v));
+  v = fmaxf(v, from_up<2>(v));
+  v = fmaxf(v, from_up<1>(v));
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ uint32_t tree_umax(uint32_t v) {
+  v = max(v, from_up<32>(v));
+  v = max(v, from_up<16>(v));
+  v = max(v, from_up<8>(v));
+  v = max(v, from_up<4>(v));
+  v = max(v, from_up<2>(v));
+  v = max(v, from_up<1>(v));
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+__device__ __forceinline__ uint32_t tree_or(uint32_t v) {
+  v |= from_up<32>(v);
+  v |= from_up<16>(v);
+  v |= from_up<8>(v);
+  v |= from_up<4>(v);
+  v |= from_up<2>(v);
+  v |= from_up<1>(v);
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
 
 __device__ __forceinline__ uint32_t ld_word(const uint32_t* p) {
@@ -107,12 +159,13 @@ __device__ __forceinline__ bool pair_has(uint64_t q, uint32_t tag) { return (uin
 
 // One round of a bounded poll: true once every lane is ready.  After
 // kSpinLimit rounds, or once another wait has failed (the error word, read
-// every 256 rounds), it records an error and lets the wave go on: its results
-// are then wrong, but the launch ends.
+// every 8192 rounds, far beyond any wait of a healthy launch), it records an
+// error and lets the wave go on: its results are then wrong, but the launch
+// ends.
 __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* ctl) {
   if (__all(ready)) return true;
   ++spin;
-  if (spin > kSpinLimit || ((spin & 255u) == 0u && ld_word(ctl + C_ERR) != 0u)) {
+  if (spin > kSpinLimit || ((spin & 8191u) == 0u && ld_word(ctl + C_ERR) != 0u)) {
     if (lane() == 0) st_word(ctl + C_ERR, 1u);
     return true;
   }
@@ -149,9 +202,19 @@ __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, in
 // at least 1/(2d) away from the next integer, far beyond the rounding error.
 __device__ __forceinline__ int small_div(int x, float inv) { return (int)(((float)x + 0.5f) * inv); }
 
+// Phase timestamps of a task (the constant-rate wall clock), when tracing:
+// 0 start, 1 weights landed (waited for only when tracing), 3 inputs polled,
+// 4 chains done, 2 end, 5 when the wave learnt the routing, 7 the wave.
 #define UOCR_TRACE(a, task, slot)                                                                          \
   do {                                                                                                     \
     if ((a).trace != nullptr && lane() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
+  } while (0)
+#define UOCR_TRACE_LOADS(a, task)                       \
+  do {                                                  \
+    if ((a).trace != nullptr) {                         \
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); \
+      UOCR_TRACE(a, task, 1);                           \
+    }                                                   \
   } while (0)
 
 // --------------------------------------------------------------------------- tasks
@@ -165,11 +228,11 @@ struct Task {
   int c;  // sgu: chunk of H
 };
 
-__device__ __forceinline__ int task_count(const FusedArgs& A, int ng) {
+__device__ __forceinline__ int task_count(const KA FusedArgs& A, int ng) {
   return A.E + A.n_sgu + ng * A.per_e_gu + A.cb_fs + A.n_sdn + ng * A.per_e_dn + A.cb_h;
 }
 
-__device__ __forceinline__ Task task_at(const FusedArgs& A, int ng, int t) {
+__device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
   if (t < A.E) return {K_ROUTER, t, 0, 0};
   t -= A.E;
   if (t < A.n_sgu) {
@@ -203,13 +266,14 @@ __device__ __forceinline__ Task task_at(const FusedArgs& A, int ng, int t) {
 
 // --------------------------------------------------------------------------- routing
 
-// The routing as every wave holds it: lane r (< B*topk) has routed row r's
-// expert, `mask` the selected experts, ng their number.  Slot s is the s-th
-// selected expert in ascending id.
+// The routing as every wave holds it: `mask` the selected experts, ng their
+// number, ids the workgroup's table of routed rows' experts (LDS, row r at
+// ids[r], B*topk rows).  Slot s is the s-th selected expert in ascending id.
 struct Route {
-  int my_id;
   uint64_t mask;
   int ng;
+  const int* ids;
+  int rows;
 };
 
 __device__ __forceinline__ int slot_expert(const Route& rt, int s) {
@@ -221,45 +285,51 @@ __device__ __forceinline__ int slot_expert(const Route& rt, int s) {
 }
 
 // Routed rows of expert e, ascending (a bit per row).
-__device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) { return __ballot(rt.my_id == e); }
+__device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) {
+  const int l = lane();
+  const int id = l < rt.rows ? rt.ids[l] : -1;
+  return __ballot(id == e);
+}
 
 // Softmax + top-k of token t from its tagged logits into the workgroup's
-// tables (same steps as route.hip's k_softmax_topk), then one more on the
-// workgroup's count of routed tokens.
-__device__ __attribute__((always_inline)) void route_token(const FusedArgs& A, int t, uint32_t tag, int* r_ids,
+// tables (same steps as route.hip's k_softmax_topk: max, exp, halving-tree
+// sum, divide; the k largest probabilities in turn, ties to the lower id),
+// then one more on the workgroup's count of routed tokens.
+__device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int t, uint32_t tag, int* r_ids,
                                                            float* r_wts, int* r_done) {
   const int l = lane();
-  const uint64_t* src = A.logits + t * 64 + (l < A.E ? l : A.E - 1);
+  const uint64_t* src = A.logits + (blockIdx.x % kLogitCopies) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
   uint64_t q;
   uint32_t spin = 0;
+  const bool wtrace = A.trace != nullptr && t == 0 && l == 0;
+  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 0] = (int64_t)wall_clock64();
   do {
     q = ld_pair(src);
   } while (!poll_done(pair_has(q, tag), spin, A.ctl));
-  const float v = l < A.E ? pair_value(q) : -__builtin_huge_valf();
-  float m = v;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, shfl(m, lane() ^ off));
-  const float ex = l < A.E ? uexp(v - m) : 0.0f;
-  const float S = shfl(tree_sum(ex), 0);
-  const float pr = l < A.E ? ex / S : 0.0f;
-  uint64_t key = l < A.E ? (((uint64_t)__float_as_uint(pr) << 32) | (uint64_t)(kWave - l)) : 0ull;
+  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 1] = (int64_t)wall_clock64();
+  const bool real = l < A.E;
+  const float v = real ? pair_value(q) : -__builtin_huge_valf();
+  const float m = tree_max(v);
+  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 3] = (int64_t)wall_clock64();
+  const float ex = real ? uexp(v - m) : 0.0f;
+  const float S = tree_sum(ex);
+  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 4] = (int64_t)wall_clock64();
+  const float pr = real ? ex / S : 0.0f;
+  bool cand = real;
   float d = 0.0f;
   for (int j = 0; j < A.topk; ++j) {
-    uint64_t best = key;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const uint64_t o = shfl(best, lane() ^ off);
-      best = o > best ? o : best;
-    }
-    const int sel = kWave - (int)(best & 0xFFFFFFFFu);
-    const float ws = shfl(pr, sel);
+    const uint32_t bits = cand ? __float_as_uint(pr) : 0u;
+    const uint32_t best = tree_umax(bits);
+    const int sel = (int)__builtin_ctzll(__ballot(cand && bits == best));
+    const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), sel));
     d = d + ws;
-    if (l == sel) key = 0ull;
+    cand = cand && l != sel;
     if (l == 0) {
       r_ids[t * A.topk + j] = sel;
       r_wts[t * A.topk + j] = ws;
     }
   }
+  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 5] = (int64_t)wall_clock64();
   if (l == 0) {
     for (int j = 0; j < A.topk; ++j) {
       const int i = t * A.topk + j;
@@ -272,18 +342,18 @@ __device__ __attribute__((always_inline)) void route_token(const FusedArgs& A, i
     // the tables are in LDS before the count says so
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __hip_atomic_fetch_add(r_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 2] = (int64_t)wall_clock64();
   }
 }
 
-__device__ __forceinline__ Route make_route(const FusedArgs& A, const int* r_ids) {
+__device__ __forceinline__ Route make_route(const KA FusedArgs& A, const int* r_ids) {
   const int l = lane();
   Route rt;
-  rt.my_id = l < A.B * A.topk ? r_ids[l] : -1;
-  uint64_t bit = rt.my_id >= 0 ? (1ull << rt.my_id) : 0ull;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) bit |= shfl(bit, lane() ^ off);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bit);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(bit >> 32));
+  rt.ids = r_ids;
+  rt.rows = A.B * A.topk;
+  const int id = l < rt.rows ? r_ids[l] : -1;
+  const uint32_t lo = tree_or(id >= 0 && id < 32 ? (1u << id) : 0u);
+  const uint32_t hi = tree_or(id >= 32 ? (1u << (id - 32)) : 0u);
   rt.mask = ((uint64_t)hi << 32) | lo;
   rt.ng = __builtin_popcountll(rt.mask);
   return rt;
@@ -305,7 +375,7 @@ __device__ __forceinline__ i32x4 ld16(const void* p) { return *(const UOCR_GLOBA
 // (int8) or 256 (bf16) contiguous bytes; lanes past the task repeat its last
 // lane's row.
 template <bool INT8>
-__device__ __attribute__((always_inline)) void issue_routed(const FusedArgs& A, bool gu, int e, int n0, int ncols,
+__device__ __attribute__((always_inline)) void issue_routed(const KA FusedArgs& A, bool gu, int e, int n0, int ncols,
                                                             Stage<INT8>& st) {
   const int l = lane();
   const int G = gu ? A.gh : A.gf;
@@ -396,16 +466,26 @@ struct Ctx {
   const float* r_wts;
   float* act;       // the wave's activation stage
   uint32_t tag;
+  int t;            // the running task (tracing)
 };
 
-__device__ __attribute__((always_inline)) void router_task(const FusedArgs& A, const Ctx& C, int e) {
-  constexpr int kMaxJ = 32;  // H <= 2048
+// Router task of expert e: the lane's router weights (k = l + 64 j), loaded
+// before the x rows are staged, then every token's logit in the 64-lane tree
+// order, stored into each copy of the logits.
+constexpr int kMaxJ = 32;  // H <= 2048
+
+__device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A, int e, float (&w)[kMaxJ]) {
   const int l = lane();
-  const float* wr = A.router + (int64_t)e * A.H;
-  const int nk = A.H / kWave;  // k = l + 64 j
-  float w[kMaxJ];
+  const float* wr = A.router + (int64_t)e * A.H + l;
+  const int nk = A.H / kWave;
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) w[j] = j < nk ? ldg(wr + l + kWave * j) : 0.0f;
+  for (int j = 0; j < kMaxJ; ++j) w[j] = ldg(wr + (j < nk ? j : nk - 1) * kWave);
+}
+
+__device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A, const Ctx& C, int e,
+                                                           const float (&w)[kMaxJ]) {
+  const int l = lane();
+  const int nk = A.H / kWave;
   for (int t = 0; t < A.B; ++t) {
     const float* xr = C.xs + t * A.gh * kXPad + l;
     float p = 0.0f;
@@ -413,27 +493,29 @@ __device__ __attribute__((always_inline)) void router_task(const FusedArgs& A, c
     for (int j = 0; j < kMaxJ; ++j)
       if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
     const float v = tree_sum(p);
-    if (l == 0) st_pair(A.logits + t * 64 + e, v, C.tag);
+    if (l < kLogitCopies) st_pair(A.logits + l * kLogitCopyWords + t * 64 + e, v, C.tag);
   }
+  UOCR_TRACE(A, C.t, 4);
 }
 
 // Shared gate or up, 64 columns x chunk g of H, every token: partials.
-__device__ __attribute__((always_inline)) void sgu_rows(const FusedArgs& A, const Ctx& C, const Task& k,
+__device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, const Ctx& C, const Task& k,
                                                         const Stage<false>& st) {
   uint64_t* dst = A.p_sgu + ((int64_t)(k.a * 2 + k.b) * A.gh + k.c) * A.B * 64 + lane();
   for (int r = 0; r < A.B; ++r)
     st_pair(dst + r * 64, chain<false>(st, C.xs + (r * A.gh + k.c) * kXPad), C.tag);
 }
 
-__device__ __attribute__((always_inline)) void task_sgu(const FusedArgs& A, const Ctx& C, const Task& k) {
+__device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   Stage<false> st;
   issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
+  UOCR_TRACE_LOADS(A, C.t);
   sgu_rows(A, C, k, st);
 }
 
 // Shared gate/up fold of 64 columns: hs = silu(sum_g gate) * (sum_g up),
 // chunk sums added in order.
-__device__ __attribute__((always_inline)) void task_sfold(const FusedArgs& A, const Ctx& C, const Task& k) {
+__device__ __attribute__((always_inline)) void task_sfold(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   constexpr int kMaxG = 16;
   const int l = lane();
   const int n = k.a * 64 + l;
@@ -455,11 +537,12 @@ __device__ __attribute__((always_inline)) void task_sfold(const FusedArgs& A, co
 }
 
 // Shared down, 64 columns x chunk g of Fs, every token: partials.
-__device__ __attribute__((always_inline)) void task_sdn(const FusedArgs& A, const Ctx& C, const Task& k) {
+__device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   const int l = lane();
   const int g = k.b;
   Stage<false> st;
   issue_kblocked(A.sh_down, A.H, k.a * 64, g, st);
+  UOCR_TRACE_LOADS(A, C.t);
   // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
   {
     // rows r0..r0+3 per round: pair i is row r0 + i/2, element (i%2)*64 + l
@@ -492,6 +575,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const FusedArgs& A, cons
     }
     __builtin_amdgcn_wave_barrier();
   }
+  UOCR_TRACE(A, C.t, 3);
   uint64_t* dst = A.p_sdn + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
   for (int r = 0; r < A.B; ++r) st_pair(dst + r * 64, chain<false>(st, C.act + r * 128), C.tag);
 }
@@ -500,7 +584,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const FusedArgs& A, cons
 // expert's routed rows: h = silu(fold(gate)) * fold(up), fold over the
 // 128-groups in order.
 template <bool INT8>
-__device__ __attribute__((always_inline)) void task_rgu(const FusedArgs& A, const Ctx& C, const Route& rt,
+__device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
   const int l = lane();
@@ -510,6 +594,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const FusedArgs& A, cons
   const int ncols = min(A.c_gu, A.F - n0);
   Stage<INT8> st;
   issue_routed<INT8>(A, true, e, n0, ncols, st);
+  UOCR_TRACE_LOADS(A, C.t);
   const int lanes = 2 * ncols * A.gh;
   const int lam = min(l, lanes - 1);
   const int cp = small_div(lam, A.inv_gh);
@@ -538,6 +623,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const FusedArgs& A, cons
           acc = acc + pv;
       }
     }
+    UOCR_TRACE(A, C.t, 4);
     const float up = shfl(acc, min(l + A.gh, kWave - 1));
     if (writer) st_pair(A.h + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
   }
@@ -546,7 +632,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const FusedArgs& A, cons
 // Routed down of one expert for c_dn columns, every chunk of F, row by row:
 // y = fold over the 128-groups in order.
 template <bool INT8>
-__device__ __attribute__((always_inline)) void task_rdn(const FusedArgs& A, const Ctx& C, const Route& rt,
+__device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
   constexpr int kMaxP = 8;  // pairs per lane per poll round
@@ -557,6 +643,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const FusedArgs& A, cons
   const int ncols = min(A.c_dn, A.H - n0);
   Stage<INT8> st;
   issue_routed<INT8>(A, false, e, n0, ncols, st);
+  UOCR_TRACE_LOADS(A, C.t);
   const int lanes = ncols * A.gf;
   const int lam = min(l, lanes - 1);
   const int c = small_div(lam, A.inv_gf);
@@ -585,6 +672,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const FusedArgs& A, cons
       }
     }
     __builtin_amdgcn_wave_barrier();
+    UOCR_TRACE(A, C.t, 3);
     const float part = chain<INT8>(st, C.act + g * kXPad);
     float acc = 0.0f;
 #pragma unroll
@@ -597,6 +685,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const FusedArgs& A, cons
           acc = acc + pv;
       }
     }
+    UOCR_TRACE(A, C.t, 4);
     if (g == 0 && l < lanes) st_pair(A.y + (int64_t)r * A.H + n0 + c, acc, C.tag);
     __builtin_amdgcn_wave_barrier();
   }
@@ -605,7 +694,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const FusedArgs& A, cons
 // 64 columns of the output: sh = shared-down chunk partials added in order;
 // out = fma chain over j of w_j * y_j from 0, plus sh.  The last comb task of
 // the launch advances the launch tag.
-__device__ __attribute__((always_inline)) void task_comb(const FusedArgs& A, const Ctx& C, const Task& k,
+__device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, const Ctx& C, const Task& k,
                                                          uint32_t epoch) {
   constexpr int kMaxG = 16;
   constexpr int kMaxK = 8;
@@ -621,6 +710,7 @@ __device__ __attribute__((always_inline)) void task_comb(const FusedArgs& A, con
       if (g < A.gfs) shv = shv + v[g];
     float y[kMaxK];
     poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, y);
+    UOCR_TRACE(A, C.t, 3);
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxK; ++j)
@@ -643,9 +733,12 @@ __device__ __attribute__((always_inline)) void task_comb(const FusedArgs& A, con
 }
 
 // Runs task t.
-__device__ __attribute__((always_inline)) void run_task(const FusedArgs& A, const Ctx& C, const Route& rt, int t,
-                                                        const Task& k, uint32_t epoch) {
+__device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, const Ctx& C0, const Route& rt, int t,
+                                                        const Task& k, uint32_t epoch, int64_t troute) {
+  Ctx C = C0;
+  C.t = t;
   UOCR_TRACE(A, t, 0);
+  if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 5] = troute;
   switch (k.kind) {
     case K_SGU: task_sgu(A, C, k); break;
     case K_RGU:
@@ -670,7 +763,10 @@ __device__ __attribute__((always_inline)) void run_task(const FusedArgs& A, cons
     A.trace[(int64_t)t * 8 + 7] = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
 }
 
-__global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs A) {
+__global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
+  (void)args;  // read in place, through the kernel-argument segment
+  const KA FusedArgs* Ap = (const KA FusedArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  const KA FusedArgs& A = *Ap;
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int wave = (int)(threadIdx.x >> 6);
   Ctx C;
@@ -684,42 +780,46 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs A) {
   C.act = (float*)(lds + A.lds_x + 528 + wave * A.lds_act);
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_word(A.ctl + C_EPOCH));
   C.tag = epoch + 1u;
+  const int nwaves = (int)gridDim.x * kWaves;
+  const int rank = wave * (int)gridDim.x + (int)blockIdx.x;
+  int t = rank;
+
+  // a router task's weights do not depend on x: they load while x is staged
+  float w[kMaxJ];
+  if (t < A.E) router_load(A, t, w);
 
   // x rows into LDS, each 128-element chunk padded to kXPad floats
   for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
-    const int t = i / A.H;
-    const int kk = i - t * A.H;
-    xs[t * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
+    const int r = i / A.H;
+    const int kk = i - r * A.H;
+    xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
   }
   if (threadIdx.x == 0) *r_done = 0;
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(A.ctl + C_ARRIVED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  const int nwaves = (int)gridDim.x * kWaves;
-  int t = wave * (int)gridDim.x + (int)blockIdx.x;
-  for (; t < A.E; t += nwaves) {
+  for (bool first = true; t < A.E; t += nwaves, first = false) {
+    C.t = t;
     UOCR_TRACE(A, t, 0);
-    router_task(A, C, t);
+    if (!first) router_load(A, t, w);
+    router_task(A, C, t, w);
     UOCR_TRACE(A, t, 2);
-    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = wave * (int)gridDim.x + (int)blockIdx.x;
+    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = rank;
   }
   // The first task after the router tasks may be a shared gate/up chunk,
-  // which does not need the routing: it runs now, its weights loading while
-  // the routing waves poll the logits.  The routing of token i is computed by
-  // wave kWaves-1-i (high waves rarely hold such a chunk).
+  // which does not need the routing: a wave that does not route runs it now.
+  // The routing of token i is computed by wave kWaves-1-i (high waves, whose
+  // first tasks come late in the list).
   const int rwave = kWaves - 1 - wave;
-  if (t < A.E + A.n_sgu) {
-    Stage<false> st;
-    const Task k = task_at(A, 0, t);
-    UOCR_TRACE(A, t, 0);
-    issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
-    if (rwave < A.B) route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
-    sgu_rows(A, C, k, st);
-    UOCR_TRACE(A, t, 2);
-    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = wave * (int)gridDim.x + (int)blockIdx.x;
-    t += nwaves;
-  } else if (rwave < A.B) {
+  if (rwave < A.B) {
     route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
+  } else if (t < A.E + A.n_sgu) {
+    C.t = t;
+    UOCR_TRACE(A, t, 0);
+    task_sgu(A, C, task_at(A, 0, t));
+    UOCR_TRACE(A, t, 2);
+    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = rank;
+    t += nwaves;
   }
   {
     uint32_t spin = 0;
@@ -728,9 +828,14 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs A) {
     }
     asm volatile("" ::: "memory");
   }
+  const int64_t troute = A.trace != nullptr ? (int64_t)wall_clock64() : 0;
   const Route rt = make_route(A, r_ids);
   const int n_tasks = task_count(A, rt.ng);
-  for (; t < n_tasks; t += nwaves) run_task(A, C, rt, t, task_at(A, rt.ng, t), epoch);
+  for (; t < n_tasks; t += nwaves) {
+    const KA FusedArgs* Ai = Ap;
+    asm volatile("" : "+s"(Ai));
+    run_task(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), epoch, troute);
+  }
 }
 
 }  // namespace
@@ -759,7 +864,7 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
   // tagged words for the largest batch (8 tokens) of this layer
   const int64_t rmax = 8 * (int64_t)topk;
   L.off_logits = 0;
-  L.off_h = L.off_logits + 8 * 64;
+  L.off_h = L.off_logits + (int64_t)kLogitCopies * kLogitCopyWords;
   L.off_y = L.off_h + rmax * F;
   L.off_hs = L.off_y + rmax * H;
   L.off_psgu = L.off_hs + 8 * (int64_t)Fs;

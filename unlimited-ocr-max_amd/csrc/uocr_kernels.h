@@ -137,8 +137,10 @@ hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared
 
 // ---- the persistent decode layer (decode.hip) ----
 
-constexpr int kFusedWaves = 16;  // waves per workgroup, one workgroup per CU
+constexpr int kFusedWaves = 12;  // waves per workgroup, one workgroup per CU (168 VGPRs a lane)
 constexpr int kFusedXPad = 132;  // floats per 128-element chunk of an LDS activation row
+constexpr int kFusedLogitCopies = 16;      // copies of the tagged logits
+constexpr int kFusedLogitCopyWords = 576;  // 64-bit words per copy (8 tokens x 64 experts, padded)
 
 // Task layout, LDS and tagged-buffer sizes of one layer shape.
 struct FusedLayout {
@@ -174,7 +176,7 @@ struct FusedArgs {
   float* wts_out;
   // library-owned, zeroed when allocated: control words and tagged pairs
   uint32_t* ctl;
-  uint64_t* logits;  // [B][64]
+  uint64_t* logits;  // [kFusedLogitCopies][kFusedLogitCopyWords]: copy c, token t, expert e at c*576 + t*64 + e
   uint64_t* h;       // [B*topk][F]
   uint64_t* y;       // [B*topk][H]
   uint64_t* hs;      // [B][Fs]
@@ -183,8 +185,10 @@ struct FusedArgs {
   // layout (FusedLayout)
   int gh, gf, gfs, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, lds_x, lds_act;
   float inv_gh, inv_gf;
-  // optional per-task phase timestamps (8 words per task), null when off
+  // optional per-task phase timestamps (8 words per task), null when off;
+  // per-workgroup words start at trace_wg
   int64_t* trace;
+  int64_t trace_wg;
 };
 hipError_t fused_grid(size_t lds_bytes, int* grid);
 hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s);

@@ -581,8 +581,9 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
     a.wts_out = expert_weights;
     {
       std::lock_guard<std::mutex> lock(g_ws_mu);
-      if (g_trace != nullptr && g_trace_words >= (int64_t)lay.max_tasks * 8) {
+      if (g_trace != nullptr && g_trace_words >= ((int64_t)lay.max_tasks + grid) * 8) {
         a.trace = g_trace;
+        a.trace_wg = (int64_t)lay.max_tasks * 8;
         g_trace = nullptr;
         g_trace_grid = grid;
       }
