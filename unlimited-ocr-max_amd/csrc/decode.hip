@@ -14,15 +14,18 @@
 // different CUs and XCDs), every wave walking its tasks in increasing order:
 //   router  one expert's logits for every token                       (E)
 //   sgu     shared gate or up: 64 columns x one 128-chunk of H         (Fs/64 x 2 x H/128)
+//   sfold   shared gate/up partials of 64 columns, one token -> SwiGLU
+//           -> hs                                                      (Fs/64 x B)
+//   sdn     shared down: 64 columns x one 128-chunk of Fs              (H/64 x Fs/128)
 //   rgu     routed gate+up of one selected expert: a few columns,
 //           every chunk of H (lane = column, projection, chunk)        (experts x F/c_gu)
-//   sfold   shared gate/up partials of 64 columns -> SwiGLU -> hs      (Fs/64)
-//   sdn     shared down: 64 columns x one 128-chunk of Fs              (H/64 x Fs/128)
 //   rdn     routed down of one selected expert: a few columns, every
 //           chunk of F (lane = column, chunk)                          (experts x H/c_dn)
-//   comb    64 columns: shared-down partials -> sh, then the weighted
-//           combine of the routed rows plus sh                         (H/64)
-// A routed task holds every chunk of its columns, so its per-group fold runs
+//   comb    64 columns, one token: shared-down partials -> sh, then the
+//           weighted combine of the token's routed rows plus sh        (H/64 x B)
+// The tasks before rgu need no routing: a wave runs those of its tasks while
+// the routing is computed.  A routed task holds every chunk of its columns, so
+// its per-group fold runs
 // inside the wave (lane shuffles); only the shared experts, whose chunks are
 // spread over tasks, fold partials written by other waves.  Each lane loads
 // the weights of its own row and chunk (128 int8 or 256 bf16 bytes, 16 bytes
@@ -39,7 +42,7 @@
 // each wait is also bounded and records an error if it ever runs out.  The
 // launch tag is the control word EPOCH + 1: every wave reads EPOCH at its
 // start, each workgroup then adds one to ARRIVED (a non-returning atomic),
-// and the last of the comb tasks (the only counter, H/64 increments) waits
+// and the last of the comb tasks (the only counter, H/64 x B increments) waits
 // for ARRIVED to reach the grid, clears both counters and advances EPOCH.
 // The tagged buffers and control words are library-owned and zeroed when
 // allocated; tags start at 1, so no zeroed word is ever taken for data.
@@ -174,12 +177,16 @@ __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* 
 }
 
 // Polls n tagged pairs p[i * stride] (i < n <= N, per lane) until all carry
-// `tag`; their values land in v[0..n).  The addresses advance from p (no
-// per-index offsets for the compiler to hoist out of the task loop).
+// `tag`; their values land in v[0..n).  It first probes only the first pair
+// of every lane, so a waiting wave reads one pair per lane per round instead
+// of n; the addresses advance from p (no per-index offsets for the compiler
+// to hoist out of the task loop).
 template <int N>
 __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, uint32_t* ctl,
                                            float (&v)[N]) {
   uint32_t spin = 0;
+  while (!poll_done(pair_has(ld_pair(p), tag), spin, ctl)) {
+  }
   for (;;) {
     uint64_t q[N];
     const uint64_t* a = p;
@@ -224,13 +231,16 @@ enum Kind : int { K_ROUTER, K_SGU, K_RGU, K_SFOLD, K_SDN, K_RDN, K_COMB, K_NONE 
 struct Task {
   int kind;
   int a;  // router: expert; sgu/sfold: column block of Fs; rgu/rdn: expert slot; sdn/comb: column block of H
-  int b;  // sgu: projection; rgu/rdn: column group; sdn: chunk of Fs
+  int b;  // sgu: projection; rgu/rdn: column group; sdn: chunk of Fs; sfold/comb: token
   int c;  // sgu: chunk of H
 };
 
 __device__ __forceinline__ int task_count(const KA FusedArgs& A, int ng) {
-  return A.E + A.n_sgu + ng * A.per_e_gu + A.cb_fs + A.n_sdn + ng * A.per_e_dn + A.cb_h;
+  return A.E + A.n_sgu + A.n_sfold + A.n_sdn + ng * A.per_e_gu + ng * A.per_e_dn + A.n_comb;
 }
+
+// Tasks that do not need the routing: the router, and the shared experts.
+__device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.E + A.n_sgu + A.n_sfold + A.n_sdn; }
 
 __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
   if (t < A.E) return {K_ROUTER, t, 0, 0};
@@ -243,24 +253,30 @@ __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
     return {K_SGU, u, p, r - p * A.gh};
   }
   t -= A.n_sgu;
-  if (t < ng * A.per_e_gu) {
-    const int s = t / A.per_e_gu;
-    return {K_RGU, s, t - s * A.per_e_gu, 0};
+  if (t < A.n_sfold) {
+    const int u = t / A.B;
+    return {K_SFOLD, u, t - u * A.B, 0};
   }
-  t -= ng * A.per_e_gu;
-  if (t < A.cb_fs) return {K_SFOLD, t, 0, 0};
-  t -= A.cb_fs;
+  t -= A.n_sfold;
   if (t < A.n_sdn) {
     const int cb = t / A.gfs;
     return {K_SDN, cb, t - cb * A.gfs, 0};
   }
   t -= A.n_sdn;
+  if (t < ng * A.per_e_gu) {
+    const int s = t / A.per_e_gu;
+    return {K_RGU, s, t - s * A.per_e_gu, 0};
+  }
+  t -= ng * A.per_e_gu;
   if (t < ng * A.per_e_dn) {
     const int s = t / A.per_e_dn;
     return {K_RDN, s, t - s * A.per_e_dn, 0};
   }
   t -= ng * A.per_e_dn;
-  if (t < A.cb_h) return {K_COMB, t, 0, 0};
+  if (t < A.n_comb) {
+    const int cb = t / A.B;
+    return {K_COMB, cb, t - cb * A.B, 0};
+  }
   return {K_NONE, 0, 0, 0};
 }
 
@@ -317,6 +333,8 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   const float pr = real ? ex / S : 0.0f;
   bool cand = real;
   float d = 0.0f;
+  int my_sel = 0;      // lane j < topk: the j-th selection
+  float my_w = 0.0f;
   for (int j = 0; j < A.topk; ++j) {
     const uint32_t bits = cand ? __float_as_uint(pr) : 0u;
     const uint32_t best = tree_umax(bits);
@@ -324,23 +342,25 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
     const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), sel));
     d = d + ws;
     cand = cand && l != sel;
-    if (l == 0) {
-      r_ids[t * A.topk + j] = sel;
-      r_wts[t * A.topk + j] = ws;
+    if (l == j) {
+      my_sel = sel;
+      my_w = ws;
     }
   }
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 5] = (int64_t)wall_clock64();
-  if (l == 0) {
-    for (int j = 0; j < A.topk; ++j) {
-      const int i = t * A.topk + j;
-      if (A.renorm) r_wts[i] = r_wts[i] / d;
-      if (blockIdx.x == 0) {
-        if (A.ids_out != nullptr) A.ids_out[i] = r_ids[i];
-        if (A.wts_out != nullptr) A.wts_out[i] = r_wts[i];
-      }
+  if (A.renorm) my_w = my_w / d;
+  if (l < A.topk) {
+    const int i = t * A.topk + l;
+    r_ids[i] = my_sel;
+    r_wts[i] = my_w;
+    if (blockIdx.x == 0) {
+      if (A.ids_out != nullptr) A.ids_out[i] = my_sel;
+      if (A.wts_out != nullptr) A.wts_out[i] = my_w;
     }
-    // the tables are in LDS before the count says so
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  // the tables are in LDS before the count says so
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (l == 0) {
     __hip_atomic_fetch_add(r_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 2] = (int64_t)wall_clock64();
   }
@@ -513,27 +533,26 @@ __device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, c
   sgu_rows(A, C, k, st);
 }
 
-// Shared gate/up fold of 64 columns: hs = silu(sum_g gate) * (sum_g up),
-// chunk sums added in order.
+// Shared gate/up fold of 64 columns for token r: hs = silu(sum_g gate) *
+// (sum_g up), chunk sums added in order.
 __device__ __attribute__((always_inline)) void task_sfold(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   constexpr int kMaxG = 16;
   const int l = lane();
-  const int n = k.a * 64 + l;
-  for (int r = 0; r < A.B; ++r) {
-    float acc[2];
+  const int r = k.b;
+  float acc[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      float v[kMaxG];
-      poll_pairs<kMaxG>(A.p_sgu + ((int64_t)(k.a * 2 + p) * A.gh * A.B + r) * 64 + l, (int64_t)A.B * 64, A.gh,
-                        C.tag, A.ctl, v);
-      float s = 0.0f;
+  for (int p = 0; p < 2; ++p) {
+    float v[kMaxG];
+    poll_pairs<kMaxG>(A.p_sgu + ((int64_t)(k.a * 2 + p) * A.gh * A.B + r) * 64 + l, (int64_t)A.B * 64, A.gh, C.tag,
+                      A.ctl, v);
+    float sum = 0.0f;
 #pragma unroll
-      for (int g = 0; g < kMaxG; ++g)
-        if (g < A.gh) s = s + v[g];
-      acc[p] = s;
-    }
-    st_pair(A.hs + (int64_t)r * A.Fs + n, silu(acc[0]) * acc[1], C.tag);
+    for (int g = 0; g < kMaxG; ++g)
+      if (g < A.gh) sum = sum + v[g];
+    acc[p] = sum;
   }
+  UOCR_TRACE(A, C.t, 3);
+  st_pair(A.hs + (int64_t)r * A.Fs + k.a * 64 + l, silu(acc[0]) * acc[1], C.tag);
 }
 
 // Shared down, 64 columns x chunk g of Fs, every token: partials.
@@ -545,34 +564,34 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   UOCR_TRACE_LOADS(A, C.t);
   // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
   {
-    // rows r0..r0+3 per round: pair i is row r0 + i/2, element (i%2)*64 + l
-    constexpr int kMaxP = 8;
-    for (int r0 = 0; r0 < A.B; r0 += kMaxP / 2) {
-      const int np = min(kMaxP, 2 * (A.B - r0));
-      const uint64_t* src = A.hs + (int64_t)r0 * A.Fs + (int64_t)g * 128 + l;
-      float v[kMaxP];
-      uint32_t spin = 0;
-      for (;;) {
-        uint64_t q[kMaxP];
-        const uint64_t* a = src;
-#pragma unroll
-        for (int i = 0; i < kMaxP; i += 2) {
-          q[i] = ld_pair(a);
-          q[i + 1] = ld_pair(a + 64);
-          if (i + 2 < np) a += A.Fs;
-        }
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < kMaxP; ++i) {
-          v[i] = pair_value(q[i]);
-          ok = ok && pair_has(q[i], C.tag);
-        }
-        if (poll_done(ok, spin, A.ctl)) break;
-      }
-#pragma unroll
-      for (int i = 0; i < kMaxP; ++i)
-        if (i < np) C.act[(r0 + (i >> 1)) * 128 + (i & 1) * 64 + l] = v[i];
+    // pair i is row i/2, element (i%2)*64 + l; the first pair is probed first
+    constexpr int kMaxP = 16;
+    const int np = 2 * A.B;
+    const uint64_t* src = A.hs + (int64_t)g * 128 + l;
+    float v[kMaxP];
+    uint32_t spin = 0;
+    while (!poll_done(pair_has(ld_pair(src), C.tag), spin, A.ctl)) {
     }
+    for (;;) {
+      uint64_t q[kMaxP];
+      const uint64_t* a = src;
+#pragma unroll
+      for (int i = 0; i < kMaxP; i += 2) {
+        q[i] = ld_pair(a);
+        q[i + 1] = ld_pair(a + 64);
+        if (i + 2 < np) a += A.Fs;
+      }
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < kMaxP; ++i) {
+        v[i] = pair_value(q[i]);
+        ok = ok && pair_has(q[i], C.tag);
+      }
+      if (poll_done(ok, spin, A.ctl)) break;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxP; ++i)
+      if (i < np) C.act[(i >> 1) * 128 + (i & 1) * 64 + l] = v[i];
     __builtin_amdgcn_wave_barrier();
   }
   UOCR_TRACE(A, C.t, 3);
@@ -691,36 +710,34 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   }
 }
 
-// 64 columns of the output: sh = shared-down chunk partials added in order;
-// out = fma chain over j of w_j * y_j from 0, plus sh.  The last comb task of
-// the launch advances the launch tag.
+// 64 columns of token t's output: sh = shared-down chunk partials added in
+// order; out = fma chain over j of w_j * y_j from 0, plus sh.  The last comb
+// task of the launch advances the launch tag.
 __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, const Ctx& C, const Task& k,
                                                          uint32_t epoch) {
   constexpr int kMaxG = 16;
   constexpr int kMaxK = 8;
   const int l = lane();
   const int n = k.a * 64 + l;
-  for (int t = 0; t < A.B; ++t) {
-    float v[kMaxG];
-    poll_pairs<kMaxG>(A.p_sdn + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag, A.ctl,
-                      v);
-    float shv = 0.0f;
+  const int t = k.b;
+  float v[kMaxG];
+  poll_pairs<kMaxG>(A.p_sdn + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag, A.ctl, v);
+  float shv = 0.0f;
 #pragma unroll
-    for (int g = 0; g < kMaxG; ++g)
-      if (g < A.gfs) shv = shv + v[g];
-    float y[kMaxK];
-    poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, y);
-    UOCR_TRACE(A, C.t, 3);
-    float acc = 0.0f;
+  for (int g = 0; g < kMaxG; ++g)
+    if (g < A.gfs) shv = shv + v[g];
+  float y[kMaxK];
+  poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, y);
+  UOCR_TRACE(A, C.t, 3);
+  float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j)
-      if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
-    A.out[(int64_t)t * A.H + n] = acc + shv;
-  }
+  for (int j = 0; j < kMaxK; ++j)
+    if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
+  A.out[(int64_t)t * A.H + n] = acc + shv;
   uint32_t old = 0;
   if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = shfl(old, 0);
-  if (old + 1u == (uint32_t)A.cb_h) {
+  if (old + 1u == (uint32_t)A.n_comb) {
     uint32_t spin = 0;
     while (!poll_done(ld_word(A.ctl + C_ARRIVED) >= gridDim.x, spin, A.ctl)) {
     }
@@ -806,32 +823,30 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     UOCR_TRACE(A, t, 2);
     if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = rank;
   }
-  // The first task after the router tasks may be a shared gate/up chunk,
-  // which does not need the routing: a wave that does not route runs it now.
   // The routing of token i is computed by wave kWaves-1-i (high waves, whose
-  // first tasks come late in the list).
+  // tasks come late in the list); the other waves meanwhile run their tasks
+  // that do not need the routing (the shared experts).
   const int rwave = kWaves - 1 - wave;
-  if (rwave < A.B) {
-    route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
-  } else if (t < A.E + A.n_sgu) {
-    C.t = t;
-    UOCR_TRACE(A, t, 0);
-    task_sgu(A, C, task_at(A, 0, t));
-    UOCR_TRACE(A, t, 2);
-    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = rank;
-    t += nwaves;
-  }
-  {
-    uint32_t spin = 0;
-    while (!poll_done(__hip_atomic_load(r_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= A.B, spin,
-                      A.ctl)) {
+  if (rwave < A.B) route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
+  // One task loop (one copy of the task code): the first routed task waits
+  // for the workgroup's routing.
+  Route rt{0ull, 0, r_ids, 0};
+  int n_tasks = unrouted_count(A);
+  bool routed = false;
+  int64_t troute = 0;
+  for (;; t += nwaves) {
+    if (!routed && t >= n_tasks) {
+      uint32_t spin = 0;
+      while (!poll_done(__hip_atomic_load(r_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= A.B, spin,
+                        A.ctl)) {
+      }
+      asm volatile("" ::: "memory");
+      if (A.trace != nullptr) troute = (int64_t)wall_clock64();
+      rt = make_route(A, r_ids);
+      n_tasks = task_count(A, rt.ng);
+      routed = true;
     }
-    asm volatile("" ::: "memory");
-  }
-  const int64_t troute = A.trace != nullptr ? (int64_t)wall_clock64() : 0;
-  const Route rt = make_route(A, r_ids);
-  const int n_tasks = task_count(A, rt.ng);
-  for (; t < n_tasks; t += nwaves) {
+    if (t >= n_tasks) break;
     const KA FusedArgs* Ai = Ap;
     asm volatile("" : "+s"(Ai));
     run_task(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), epoch, troute);
@@ -853,6 +868,8 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
   L.cb_h = H / 64;
   L.n_sgu = L.cb_fs * 2 * L.gh;
   L.n_sdn = L.cb_h * L.gfs;
+  L.n_sfold = L.cb_fs * B;
+  L.n_comb = L.cb_h * B;
   L.lds_x = B * L.gh * kXPad * 4;
   const int act_rows = B * 128 * 4;
   const int act_h = L.gf * kXPad * 4;
@@ -860,7 +877,7 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
   L.lds_bytes = (size_t)L.lds_x + 528 + (size_t)kWaves * L.lds_act;
   const int R = B * topk;
   const int slots = E < R ? E : R;
-  L.max_tasks = E + L.n_sgu + slots * L.per_e_gu + L.cb_fs + L.n_sdn + slots * L.per_e_dn + L.cb_h;
+  L.max_tasks = E + L.n_sgu + L.n_sfold + L.n_sdn + slots * (L.per_e_gu + L.per_e_dn) + L.n_comb;
   // tagged words for the largest batch (8 tokens) of this layer
   const int64_t rmax = 8 * (int64_t)topk;
   L.off_logits = 0;

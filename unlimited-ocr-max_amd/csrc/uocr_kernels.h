@@ -149,6 +149,7 @@ struct FusedLayout {
   int per_e_gu, per_e_dn;   // routed tasks per selected expert
   int cb_fs, cb_h;          // 64-column blocks of Fs and H
   int n_sgu, n_sdn;         // shared chunk tasks
+  int n_sfold, n_comb;      // per-token fold and combine tasks
   int lds_x, lds_act;       // LDS bytes: x rows, per-wave activation stage
   size_t lds_bytes;
   int max_tasks;
@@ -183,7 +184,7 @@ struct FusedArgs {
   uint64_t* p_sgu;   // [Fs/64][2][H/128][B][64]
   uint64_t* p_sdn;   // [H/64][Fs/128][B][64]
   // layout (FusedLayout)
-  int gh, gf, gfs, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, lds_x, lds_act;
+  int gh, gf, gfs, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, n_sfold, n_comb, lds_x, lds_act;
   float inv_gh, inv_gf;
   // optional per-task phase timestamps (8 words per task), null when off;
   // per-workgroup words start at trace_wg

@@ -486,6 +486,8 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.cb_h = lay.cb_h;
   a.n_sgu = lay.n_sgu;
   a.n_sdn = lay.n_sdn;
+  a.n_sfold = lay.n_sfold;
+  a.n_comb = lay.n_comb;
   a.lds_x = lay.lds_x;
   a.lds_act = lay.lds_act;
   a.inv_gh = 1.0f / (float)lay.gh;
