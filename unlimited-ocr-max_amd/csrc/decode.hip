@@ -172,7 +172,7 @@ __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* 
     if (lane() == 0) st_word(ctl + C_ERR, 1u);
     return true;
   }
-  __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_s_sleep(2);
   return false;
 }
 
@@ -426,6 +426,20 @@ __device__ __forceinline__ void issue_kblocked(const uint16_t* w, int N, int n0,
 
 // ---------------------------------------------------------------------------- chains
 
+// Makes the weight registers opaque (an empty asm that "modifies" them in
+// place): whatever is computed from them cannot be hoisted out of the loop
+// the call sits in.
+__device__ __forceinline__ void launder(Stage<true>& st) {
+  asm volatile("" : "+v"(st.v[0]), "+v"(st.v[1]), "+v"(st.v[2]), "+v"(st.v[3]), "+v"(st.v[4]), "+v"(st.v[5]),
+               "+v"(st.v[6]), "+v"(st.v[7]));
+}
+__device__ __forceinline__ void launder(Stage<false>& st) {
+  asm volatile("" : "+v"(st.v[0]), "+v"(st.v[1]), "+v"(st.v[2]), "+v"(st.v[3]), "+v"(st.v[4]), "+v"(st.v[5]),
+               "+v"(st.v[6]), "+v"(st.v[7]));
+  asm volatile("" : "+v"(st.v[8]), "+v"(st.v[9]), "+v"(st.v[10]), "+v"(st.v[11]), "+v"(st.v[12]), "+v"(st.v[13]),
+               "+v"(st.v[14]), "+v"(st.v[15]));
+}
+
 // The fp32 chain of one row over the lane's chunk, in k order: acc =
 // fma(w_k, x_k, acc) from 0, x_k at xp[k] (LDS).  The activations of piece
 // q+1 are read while piece q is computed; their offset passes through an
@@ -452,8 +466,7 @@ __device__ __forceinline__ float chain(const Stage<INT8>& st, const float* xp) {
 #pragma unroll
       for (int v = 0; v < NV; ++v) nxt[v] = *(const f32x4*)(xp + off + 4 * v);
     }
-    i32x4 wq = st.v[q];
-    asm volatile("" : "+v"(wq));
+    const i32x4 wq = st.v[q];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       float w[4];
@@ -520,10 +533,12 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
 
 // Shared gate or up, 64 columns x chunk g of H, every token: partials.
 __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, const Ctx& C, const Task& k,
-                                                        const Stage<false>& st) {
+                                                        Stage<false>& st) {
   uint64_t* dst = A.p_sgu + ((int64_t)(k.a * 2 + k.b) * A.gh + k.c) * A.B * 64 + lane();
-  for (int r = 0; r < A.B; ++r)
+  for (int r = 0; r < A.B; ++r) {
+    launder(st);
     st_pair(dst + r * 64, chain<false>(st, C.xs + (r * A.gh + k.c) * kXPad), C.tag);
+  }
 }
 
 __device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, const Ctx& C, const Task& k) {
@@ -596,7 +611,10 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   }
   UOCR_TRACE(A, C.t, 3);
   uint64_t* dst = A.p_sdn + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
-  for (int r = 0; r < A.B; ++r) st_pair(dst + r * 64, chain<false>(st, C.act + r * 128), C.tag);
+  for (int r = 0; r < A.B; ++r) {
+    launder(st);
+    st_pair(dst + r * 64, chain<false>(st, C.act + r * 128), C.tag);
+  }
 }
 
 // Routed gate+up of one expert for c_gu columns, every chunk of H, the
@@ -630,6 +648,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
   while (rows != 0ull) {
     const int r = (int)__builtin_ctzll(rows);
     rows &= rows - 1ull;
+    launder(st);
     const float part = chain<INT8>(st, C.xs + ((r / A.topk) * A.gh + g) * kXPad);
     float acc = 0.0f;
 #pragma unroll
@@ -692,6 +711,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     }
     __builtin_amdgcn_wave_barrier();
     UOCR_TRACE(A, C.t, 3);
+    launder(st);
     const float part = chain<INT8>(st, C.act + g * kXPad);
     float acc = 0.0f;
 #pragma unroll
