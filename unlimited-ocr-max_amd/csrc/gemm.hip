@@ -1,16 +1,14 @@
 // Prefill-shape expert contractions on the bf16 matrix cores, and the
 // standalone int8 dequantisation op.
 //
-// Grouped GEMM: the routed rows are grouped by expert (route.hip); a
-// workgroup owns a 64-row tile of one expert's rows and a 128-column tile of
-// its weights.  Per 64-wide K step it dequantises the int8 weight tile with the
-// reference's prefill numerics, w = bf16_rne(f32(q) * scale)
-// (unlimited_ocr_max/kernels/moe_int8.mojo:340, the int8_dequant_expert values),
-// into LDS, rounds the activations to bf16, and runs
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation.  The gate/up launch fuses
-// SwiGLU into its epilogue and writes h in bf16, already packed in group order,
-// which is the down launch's A operand.  The shared experts (K-blocked bf16)
-// ride in the same launches as extra tiles with every token as a row.
+// Grouped GEMM: the routed rows are grouped by expert (route.hip).  Weights
+// are dequantised with the reference's prefill numerics, w = bf16_rne(f32(q) *
+// scale) (unlimited_ocr_max/kernels/moe_int8.mojo:340, the int8_dequant_expert
+// values), activations rounded to bf16, and v_mfma_f32_32x32x16_bf16
+// accumulates in fp32.  The gate/up launch fuses SwiGLU into its epilogue and
+// writes h in bf16, already packed in group order, which is the down launch's
+// A operand.  The shared experts (K-blocked bf16) ride in the same launches as
+// extra tiles with every token as a row.
 #include "uocr_device.h"
 #include "uocr_kernels.h"
 
@@ -18,11 +16,6 @@ namespace uocr {
 
 namespace {
 
-constexpr int BM = 64;
-constexpr int BN = 128;
-constexpr int BK = 64;
-constexpr int LDA = BK + 8;  // bf16 elements per LDS row (16-byte pad)
-constexpr int kGemmThreads = 256;
 
 // ------------------------------------------------------------- dequant op
 
@@ -74,21 +67,50 @@ __global__ void __launch_bounds__(256) k_dequant(void* __restrict__ out, int out
 }
 
 // ------------------------------------------------------------- grouped GEMM
+//
+// A workgroup owns a BM-row tile of one expert's rows (or of the tokens, for
+// the shared experts) and 128 weight rows: 64 columns of both gate and up
+// (SwiGLU launch) or 128 columns of down.  Its waves form a (BM/32) x 2 grid,
+// each computing 32 rows x 32 columns of both projections (or 32 x 64 of
+// down) with v_mfma_f32_32x32x16_bf16.  K advances in steps of BK = 128 (one
+// int8 quantisation group of 128, or half of one of 256, ...): the raw global
+// data of step k+1 (bf16 activations, int8 or bf16 weights and the step's
+// scales) is loaded into registers while the matrix cores work on step k,
+// then converted (weights to bf16_rne(f32(q) * scale)) into the single LDS
+// tile.  Workgroups are dealt to XCDs so that all column tiles of one row
+// tile run on the same XCD: the activation tile they share stays in its L2.
+
+constexpr int BK = 128;
+constexpr int kRow = BK + 8;   // bf16 per LDS row (272 bytes: rows 4 banks apart)
+constexpr int kBRows = 128;    // weight rows per workgroup
+constexpr int kWN = kBRows / 64;  // waves along the columns
+constexpr int kXcds = 8;
+
+template <int BM>
+struct Geo {
+  static constexpr int kWaves = BM / 32 * kWN;
+  static constexpr int kThreads = kWaves * 64;
+};
 
 struct TileRef {
   int valid;
-  int e;        // expert (routed) or 0
-  int pos0;     // first row position of the tile (group order) or first token
-  int rows;     // valid rows in the tile
-  int n0;       // first output column
+  int e;     // expert (routed) or 0
+  int pos0;  // first row position of the tile (group order) or first token
+  int rows;  // valid rows in the tile
+  int n0;    // first output column
 };
 
-// Decodes workgroup `wg` of a problem into its tile.
-__device__ TileRef locate(const GemmProblem& P, int wg) {
+// The tile of workgroup `wg` of a problem with `mtiles` row tiles and `ntiles`
+// column tiles of width bn: workgroup w runs on XCD w % 8, and XCD x takes
+// the row tiles x, x+8, ... with all their column tiles in turn.
+template <int BM>
+__device__ TileRef locate(const GemmProblem& P, int wg, int bn) {
   TileRef t{0, 0, 0, 0, 0};
-  const int ntiles = P.N / BN;
-  const int mt = wg / ntiles;
-  t.n0 = (wg - mt * ntiles) * BN;
+  const int ntiles = P.N / bn;
+  const int x = wg % kXcds;
+  const int j = wg / kXcds;  // the j-th workgroup of XCD x
+  const int mt = x + kXcds * (j / ntiles);
+  t.n0 = (j % ntiles) * bn;
   if (P.rows.n_groups == nullptr) {
     t.pos0 = mt * BM;
     if (t.pos0 >= P.M) return t;
@@ -98,8 +120,15 @@ __device__ TileRef locate(const GemmProblem& P, int wg) {
   }
   const int ng = ldc(P.rows.n_groups);
   if (mt >= ldc(P.tile_start + ng)) return t;
-  int g = 0;
-  while (g + 1 < ng && ldc(P.tile_start + g + 1) <= mt) ++g;
+  int lo = 0, hi = ng - 1;  // the group g with tile_start[g] <= mt < tile_start[g + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (ldc(P.tile_start + mid) <= mt)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  const int g = lo;
   const int start = ldc(P.rows.group_start + g);
   const int count = ldc(P.rows.group_start + g + 1) - start;
   const int local = mt - ldc(P.tile_start + g);
@@ -110,164 +139,201 @@ __device__ TileRef locate(const GemmProblem& P, int wg) {
   return t;
 }
 
-template <WKind W, int NPROJ>
-__device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds) {
-  uint16_t* As = lds;                         // [BM][LDA]
-  uint16_t* Bs = lds + BM * LDA;              // [NPROJ][BN][LDA]
+// Workgroups of a problem: row tiles rounded up to whole XCD rounds.
+__host__ __device__ inline int grid_of(int mtiles, int ntiles) {
+  return ((mtiles + kXcds - 1) / kXcds) * kXcds * ntiles;
+}
+
+// Raw global data of one K step, per thread.
+template <int BM, WKind W>
+struct StepRegs {
+  static constexpr int kThreads = Geo<BM>::kThreads;
+  static constexpr int kAParts = kThreads / BM;                     // threads per activation row (8)
+  static constexpr int kABytes = BK * 2 / kAParts;                  // 32
+  static constexpr int kBBytes = kBRows * BK * (W == kInt8Rows ? 1 : 2) / kThreads;
+  i32x4 a[kABytes / 16];
+  i32x4 b[kBBytes / 16];
+  float scale;
+};
+
+template <int BM, WKind W, int NPROJ>
+__device__ __forceinline__ void load_step(const GemmProblem& P, const TileRef& t, const uint16_t* a_src, int k0,
+                                          StepRegs<BM, W>& R) {
+  using S = StepRegs<BM, W>;
+  constexpr int T = S::kThreads;
   const int tid = (int)threadIdx.x;
-  const int lane = lane_id();
-  const int w = tid >> 6;
-  const int wm = w & 1;   // 32-row half of the tile
-  const int wn = w >> 1;  // 64-column half of the tile
-
-  // ---- A-loader coordinates: 64 rows x 64 k, 4 threads per row, 16 k each
-  const int a_row = tid >> 2;
-  const int a_k = (tid & 3) * 16;
-  const int a_rc = min(a_row, t.rows - 1);  // padded rows repeat the last real row
-  const float* a_src_f = nullptr;
-  const uint16_t* a_src_b = nullptr;
-  if (P.x != nullptr) {
-    int token;
-    if (P.rows.n_groups == nullptr)
-      token = t.pos0 + a_rc;
-    else
-      token = ldg(P.rows.group_rows + t.pos0 + a_rc) / P.x_div;
-    a_src_f = P.x + (int64_t)token * P.ldx + a_k;
+#pragma unroll
+  for (int i = 0; i < S::kABytes / 16; ++i) R.a[i] = *(const UOCR_GLOBAL i32x4*)(a_src + k0 + 8 * i);
+  constexpr int NB = S::kBBytes / 16;
+  if constexpr (W == kBf16KBlocked) {
+    // K-blocked [K/16][N][16]: 8 blocks x 256 rows x 32 bytes; thread -> block,
+    // consecutive rows (contiguous in memory)
+    constexpr int kRowsPer = kBRows * 8 / T;
+    constexpr int kPerBlock = kBRows / kRowsPer;
+    const int kb = tid / kPerBlock;
+    const int r0 = (tid % kPerBlock) * kRowsPer;
+    const int half = kBRows / NPROJ;
+    const int p = NPROJ == 2 ? r0 / half : 0;
+    const int n = t.n0 + (NPROJ == 2 ? r0 % half : r0);
+    const uint16_t* src = (const uint16_t*)P.p[p].w + ((int64_t)(k0 / 16 + kb) * P.N + n) * 16;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) R.b[i] = *(const UOCR_GLOBAL i32x4*)(src + 8 * i);
   } else {
-    a_src_b = P.hb + (int64_t)(t.pos0 + a_rc) * P.ldh + a_k;
-  }
-
-  // ---- B-loader coordinates
-  // int8 rows: 128 rows x 64 k bytes, 2 threads per row, 32 k each
-  // bf16 rows: 128 rows x 64 k, 2 threads per row, 32 k (64 bytes) each
-  // bf16 K-blocked: 4 blocks of 16 k; thread -> (block tid/64, rows 2*(tid%64), +1)
-  const int b_row = tid >> 1;
-  const int b_k = (tid & 1) * 32;
-
-  f32x16 acc[NPROJ][2];
+    constexpr int kParts = T / kBRows;  // threads per weight row
+    const int row = tid / kParts;
+    const int part = tid % kParts;
+    const int half = kBRows / NPROJ;
+    const int p = NPROJ == 2 ? row / half : 0;
+    const int n = t.n0 + (NPROJ == 2 ? row % half : row);
+    constexpr int kEsz = W == kInt8Rows ? 1 : 2;
+    const char* src =
+        (const char*)P.p[p].w + (((int64_t)t.e * P.N + n) * P.K + k0) * kEsz + part * S::kBBytes;
 #pragma unroll
-  for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[p][c][i] = 0.0f;
-
-  const int ksteps = P.K / BK;
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const int k0 = ks * BK;
-    // ---------------- global -> LDS: A
-    {
-      uint4 packed[2];
-      if (a_src_f != nullptr) {
-        const float4* src = (const float4*)(a_src_f + k0);
-        const float4 v0 = ldg_f4(src), v1 = ldg_f4(src + 1), v2 = ldg_f4(src + 2), v3 = ldg_f4(src + 3);
-        packed[0] = make_uint4(pack_bf16x2(v0.x, v0.y), pack_bf16x2(v0.z, v0.w), pack_bf16x2(v1.x, v1.y),
-                               pack_bf16x2(v1.z, v1.w));
-        packed[1] = make_uint4(pack_bf16x2(v2.x, v2.y), pack_bf16x2(v2.z, v2.w), pack_bf16x2(v3.x, v3.y),
-                               pack_bf16x2(v3.z, v3.w));
-      } else {
-        const uint4* src = (const uint4*)(a_src_b + k0);
-        packed[0] = ldg_u4(src);
-        packed[1] = ldg_u4(src + 1);
-      }
-      uint4* dst = (uint4*)(As + a_row * LDA + a_k);
-      dst[0] = packed[0];
-      dst[1] = packed[1];
-    }
-    // ---------------- global -> LDS: B (dequantised)
-#pragma unroll
-    for (int p = 0; p < NPROJ; ++p) {
-      uint16_t* Bp = Bs + p * BN * LDA;
-      if constexpr (W == kInt8Rows) {
-        const int n = t.n0 + b_row;
-        const int8_t* src = (const int8_t*)P.p[p].w + ((int64_t)t.e * P.N + n) * P.K + k0 + b_k;
-        const float s = ldg(P.p[p].s + ((int64_t)t.e * P.N + n) * P.groups + k0 / (P.K / P.groups));
-        const int4 q0 = load_nt16(src);
-        const int4 q1 = load_nt16(src + 16);
-        const int qs[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        uint32_t o[16];
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-          const int v = qs[d];
-          o[2 * d] = pack_bf16x2((float)(int8_t)v * s, (float)(int8_t)(v >> 8) * s);
-          o[2 * d + 1] = pack_bf16x2((float)(int8_t)(v >> 16) * s, (float)(int8_t)(v >> 24) * s);
-        }
-        uint4* dst = (uint4*)(Bp + b_row * LDA + b_k);
-#pragma unroll
-        for (int d = 0; d < 4; ++d) dst[d] = make_uint4(o[4 * d], o[4 * d + 1], o[4 * d + 2], o[4 * d + 3]);
-      } else if constexpr (W == kBf16Rows) {
-        const int n = t.n0 + b_row;
-        const uint4* src =
-            (const uint4*)((const uint16_t*)P.p[p].w + ((int64_t)t.e * P.N + n) * P.K + k0 + b_k);
-        uint4* dst = (uint4*)(Bp + b_row * LDA + b_k);
-#pragma unroll
-        for (int d = 0; d < 4; ++d) dst[d] = load_nt16u(src + d);
-      } else {
-        const int kb = tid >> 6;            // which 16-wide K block of the step
-        const int nr = (tid & 63) * 2;      // two adjacent rows
-        const uint4* src = (const uint4*)((const uint16_t*)P.p[p].w +
-                                          ((int64_t)(k0 / 16 + kb) * P.N + t.n0 + nr) * 16);
-        const uint4 r0 = load_nt16u(src), r1 = load_nt16u(src + 1);
-        const uint4 r2 = load_nt16u(src + 2), r3 = load_nt16u(src + 3);
-        uint4* d0 = (uint4*)(Bp + nr * LDA + kb * 16);
-        uint4* d1 = (uint4*)(Bp + (nr + 1) * LDA + kb * 16);
-        d0[0] = r0;
-        d0[1] = r1;
-        d1[0] = r2;
-        d1[1] = r3;
-      }
-    }
-    __syncthreads();
-    // ---------------- MFMA over the step: 4 x k16
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      const int kofs = kk + (lane >> 5) * 8;
-      const bf16x8 a = *(const bf16x8*)(As + (wm * 32 + (lane & 31)) * LDA + kofs);
-#pragma unroll
-      for (int p = 0; p < NPROJ; ++p) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const bf16x8 b = *(const bf16x8*)(Bs + p * BN * LDA + (wn * 64 + c * 32 + (lane & 31)) * LDA + kofs);
-          acc[p][c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[p][c], 0, 0, 0);
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---------------- epilogue: C[i][j], lane = j + 32*(i/4 % 2), reg = 4*(i/8) + i%4
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int col = t.n0 + wn * 64 + c * 32 + (lane & 31);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const int row = wm * 32 + i;
-      if (row >= t.rows) continue;
-      const int64_t orow = (int64_t)(t.pos0 + row);
-      if constexpr (NPROJ == 2) {
-        const float h = silu(acc[0][c][r]) * acc[1][c][r];
-        stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(h));
-      } else {
-        stg(P.outf + orow * P.ldo + col, acc[0][c][r]);
-      }
+    for (int i = 0; i < NB; ++i) R.b[i] = *(const UOCR_GLOBAL i32x4*)(src + 16 * i);
+    if constexpr (W == kInt8Rows) {
+      const int gsize = P.K / P.groups;
+      const int kk = k0 + part * S::kBBytes;
+      R.scale = ldg(P.p[p].s + ((int64_t)t.e * P.N + n) * P.groups + kk / gsize);
     }
   }
 }
 
-template <WKind W0, int NP, WKind W1>
-__global__ void __launch_bounds__(kGemmThreads) k_gemm_pair(GemmProblem a, GemmProblem b, int split) {
+template <int BM, WKind W>
+__device__ __forceinline__ void store_step(const StepRegs<BM, W>& R, uint16_t* As, uint16_t* Bs) {
+  using S = StepRegs<BM, W>;
+  constexpr int T = S::kThreads;
+  const int tid = (int)threadIdx.x;
+  {
+    i32x4* dst = (i32x4*)(As + (tid / S::kAParts) * kRow + (tid % S::kAParts) * (S::kABytes / 2));
+#pragma unroll
+    for (int i = 0; i < S::kABytes / 16; ++i) dst[i] = R.a[i];
+  }
+  constexpr int NB = S::kBBytes / 16;
+  if constexpr (W == kBf16KBlocked) {
+    constexpr int kRowsPer = kBRows * 8 / T;
+    constexpr int kPerBlock = kBRows / kRowsPer;
+    const int kb = tid / kPerBlock;
+    const int r0 = (tid % kPerBlock) * kRowsPer;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) *(i32x4*)(Bs + (r0 + i / 2) * kRow + kb * 16 + (i & 1) * 8) = R.b[i];
+  } else if constexpr (W == kBf16Rows) {
+    constexpr int kParts = T / kBRows;
+    const int row = tid / kParts, part = tid % kParts;
+    i32x4* dst = (i32x4*)(Bs + row * kRow + part * (BK / kParts));
+#pragma unroll
+    for (int i = 0; i < NB; ++i) dst[i] = R.b[i];
+  } else {
+    // int8: 16 weights per piece -> 2 x 16 bytes of bf16
+    constexpr int kParts = T / kBRows;
+    const int row = tid / kParts, part = tid % kParts;
+    i32x4* dst = (i32x4*)(Bs + row * kRow + part * (BK / kParts));
+    const float s = R.scale;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      uint32_t o[8];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int v = R.b[i][d];
+        o[2 * d] = pack_bf16x2((float)(int8_t)v * s, (float)(int8_t)(v >> 8) * s);
+        o[2 * d + 1] = pack_bf16x2((float)(int8_t)(v >> 16) * s, (float)(int8_t)(v >> 24) * s);
+      }
+      dst[2 * i] = i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+      dst[2 * i + 1] = i32x4{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+    }
+  }
+}
+
+template <int BM, WKind W, int NPROJ>
+__device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds) {
+  using S = StepRegs<BM, W>;
+  uint16_t* As = lds;               // [BM][kRow]
+  uint16_t* Bs = lds + BM * kRow;   // [kBRows][kRow]
+  const int tid = (int)threadIdx.x;
+  const int lane = lane_id();
+  const int w = tid >> 6;
+  const int wm = w / kWN;  // 32-row slice
+  const int wn = w % kWN;  // column slice
+
+  // this thread's activation row (padded rows repeat the last real one)
+  const int a_pos = t.pos0 + min(tid / S::kAParts, t.rows - 1);
+  const int a_row =
+      (P.a_by_token && P.rows.n_groups != nullptr) ? ldg(P.rows.group_rows + a_pos) / P.x_div : a_pos;
+  const uint16_t* a_src = P.a + (int64_t)a_row * P.lda + (tid % S::kAParts) * (S::kABytes / 2);
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[c][i] = 0.0f;
+  // LDS rows of this wave's two 32-column B tiles
+  const int brow0 = NPROJ == 2 ? wn * 32 : wn * 64;
+  const int brow1 = NPROJ == 2 ? kBRows / 2 + wn * 32 : wn * 64 + 32;
+
+  S R;
+  load_step<BM, W, NPROJ>(P, t, a_src, 0, R);
+  const int ksteps = P.K / BK;
+  for (int ks = 0; ks < ksteps; ++ks) {
+    if (ks > 0) __syncthreads();
+    store_step<BM, W>(R, As, Bs);
+    if (ks + 1 < ksteps) load_step<BM, W, NPROJ>(P, t, a_src, (ks + 1) * BK, R);
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      const int kofs = kk + (lane >> 5) * 8;
+      const bf16x8 a = *(const bf16x8*)(As + (wm * 32 + (lane & 31)) * kRow + kofs);
+      const bf16x8 b0 = *(const bf16x8*)(Bs + (brow0 + (lane & 31)) * kRow + kofs);
+      const bf16x8 b1 = *(const bf16x8*)(Bs + (brow1 + (lane & 31)) * kRow + kofs);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc[1], 0, 0, 0);
+    }
+  }
+
+  // ---------------- epilogue: C[i][j], lane = j + 32*(i/4 % 2), reg = 4*(i/8) + i%4
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    const int row = wm * 32 + i;
+    if (row >= t.rows) continue;
+    const int64_t orow = (int64_t)(t.pos0 + row);
+    if constexpr (NPROJ == 2) {
+      const int col = t.n0 + wn * 32 + (lane & 31);
+      stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(silu(acc[0][r]) * acc[1][r]));
+    } else {
+      const int col = t.n0 + wn * 64 + (lane & 31);
+      stg(P.outf + orow * P.ldo + col, acc[0][r]);
+      stg(P.outf + orow * P.ldo + col + 32, acc[1][r]);
+    }
+  }
+}
+
+template <int BM, WKind W0, int NP, WKind W1>
+__global__ void __launch_bounds__(Geo<BM>::kThreads) k_gemm_pair(GemmProblem a, GemmProblem b, int split) {
   extern __shared__ uint16_t lds[];
+  constexpr int bn = kBRows / NP;
   const int wg = (int)blockIdx.x;
   if (wg < split) {
-    const TileRef t = locate(a, wg);
+    const TileRef t = locate<BM>(a, wg, bn);
     if (!t.valid) return;
-    gemm_tile<W0, NP>(a, t, lds);
+    gemm_tile<BM, W0, NP>(a, t, lds);
   } else {
-    const TileRef t = locate(b, wg - split);
+    const TileRef t = locate<BM>(b, wg - split, bn);
     if (!t.valid) return;
-    gemm_tile<W1, NP>(b, t, lds);
+    gemm_tile<BM, W1, NP>(b, t, lds);
   }
+}
+
+template <int BM, WKind W0, int NP>
+hipError_t launch_pair_bm(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles, hipStream_t s,
+                          const char* name) {
+  constexpr int bn = kBRows / NP;
+  const int split = grid_of(max_mtiles, routed.N / bn);
+  const int shared_wgs = grid_of((shared.M + BM - 1) / BM, shared.N / bn);
+  const int wgs = split + shared_wgs;
+  if (wgs == 0) return hipSuccess;
+  const size_t lds = (size_t)(BM + kBRows) * kRow * sizeof(uint16_t);
+  UOCR_LAUNCH(name, (k_gemm_pair<BM, W0, NP, kBf16KBlocked>), dim3(wgs), dim3(Geo<BM>::kThreads), lds, s, routed,
+              shared, split);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -282,30 +348,24 @@ hipError_t launch_dequant(void* out, int out_f32, const int8_t* w, const float* 
   return hipGetLastError();
 }
 
-int gemm_bm() { return BM; }
-int gemm_bn() { return BN; }
 int gemm_bk() { return BK; }
 
-hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles, hipStream_t s) {
-  const int nproj = routed.swiglu ? 2 : 1;
-  const int split = max_mtiles * (routed.N / BN);
-  const int shared_wgs = ((shared.M + BM - 1) / BM) * (shared.N / BN);
-  const int wgs = split + shared_wgs;
-  if (wgs == 0) return hipSuccess;
-  const size_t lds = (size_t)(BM + nproj * BN) * LDA * sizeof(uint16_t);
-  const dim3 grid(wgs), block(kGemmThreads);
-  if (routed.kind == kInt8Rows) {
-    if (nproj == 2)
-      UOCR_LAUNCH("gemm_gateup", (k_gemm_pair<kInt8Rows, 2, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
-    else
-      UOCR_LAUNCH("gemm_down", (k_gemm_pair<kInt8Rows, 1, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
-  } else {
-    if (nproj == 2)
-      UOCR_LAUNCH("gemm_gateup", (k_gemm_pair<kBf16Rows, 2, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
-    else
-      UOCR_LAUNCH("gemm_down", (k_gemm_pair<kBf16Rows, 1, kBf16KBlocked>), grid, block, lds, s, routed, shared, split);
+hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
+                            hipStream_t s) {
+  const bool gu = routed.swiglu != 0;
+  const char* name = gu ? "gemm_gateup" : "gemm_down";
+  if (bm == 128) {
+    if (routed.kind == kInt8Rows)
+      return gu ? launch_pair_bm<128, kInt8Rows, 2>(routed, shared, max_mtiles, s, name)
+                : launch_pair_bm<128, kInt8Rows, 1>(routed, shared, max_mtiles, s, name);
+    return gu ? launch_pair_bm<128, kBf16Rows, 2>(routed, shared, max_mtiles, s, name)
+              : launch_pair_bm<128, kBf16Rows, 1>(routed, shared, max_mtiles, s, name);
   }
-  return hipGetLastError();
+  if (routed.kind == kInt8Rows)
+    return gu ? launch_pair_bm<64, kInt8Rows, 2>(routed, shared, max_mtiles, s, name)
+              : launch_pair_bm<64, kInt8Rows, 1>(routed, shared, max_mtiles, s, name);
+  return gu ? launch_pair_bm<64, kBf16Rows, 2>(routed, shared, max_mtiles, s, name)
+            : launch_pair_bm<64, kBf16Rows, 1>(routed, shared, max_mtiles, s, name);
 }
 
 }  // namespace uocr

@@ -18,6 +18,62 @@ namespace {
 
 // ---------------------------------------------------------------- logits
 
+// logits[t][e] for 4 tokens x 4 experts per wave (grid: 16 experts per
+// workgroup in x, 4 tokens in y), H <= kLogitsMaxH: the lane's x and router
+// values (k = lane + 64 j) are all loaded before the fmas, then each (t, e)
+// is the 64-lane tree (DPP, the order of wave_tree_sum).  The waves of the
+// first expert group also write the tokens' x rows rounded to bf16 (xb),
+// when asked: the prefill GEMM's A operand.
+constexpr int kLogitsMaxH = 2048;
+
+template <int kJ>  // >= H / 64
+__global__ void __launch_bounds__(256) k_logits_wide(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                                     const float* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ router, int T, int E, int H) {
+  const int w = (int)(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int e0 = (int)blockIdx.x * 16 + w * 4;
+  const int t0 = (int)blockIdx.y * 4;
+  if (e0 >= E) return;
+  const int nj = H / kWave;
+  float xv[4][kJ], wv[4][kJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float* xr = x + (int64_t)min(t0 + i, T - 1) * ldx + l;
+    const float* wr = router + (int64_t)min(e0 + i, E - 1) * H + l;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      if (j < nj) {
+        xv[i][j] = ldg(xr + kWave * j);
+        wv[i][j] = ldg(wr + kWave * j);
+      }
+    }
+  }
+  if (xb != nullptr && blockIdx.x == 0 && w == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (t0 + i < T) {
+        uint16_t* dst = xb + (int64_t)(t0 + i) * H + l;
+#pragma unroll
+        for (int j = 0; j < kJ; ++j)
+          if (j < nj) dst[kWave * j] = f32_to_bf16_rne(xv[i][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+    for (int ei = 0; ei < 4; ++ei) {
+      float p = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j)
+        if (j < nj) p = __builtin_fmaf(xv[ti][j], wv[ei][j], p);
+      const float v = tree_sum(p);
+      if (l == 0 && t0 + ti < T && e0 + ei < E) logits[(int64_t)(t0 + ti) * E + e0 + ei] = v;
+    }
+  }
+}
+
 template <int TT, int EE>
 __global__ void __launch_bounds__(256) k_logits(float* __restrict__ logits, const float* __restrict__ x,
                                                 int64_t ldx, const float* __restrict__ router, int T, int E,
@@ -206,14 +262,27 @@ __global__ void __launch_bounds__(256) k_combine(float* __restrict__ out, const 
 }  // namespace
 
 hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E, int H,
-                         hipStream_t s) {
+                         uint16_t* xb, hipStream_t s) {
   if (T <= 0) return hipSuccess;
+  if (H % kWave == 0 && H <= kLogitsMaxH && (xb != nullptr || T > 8)) {
+    // every wave: 4 tokens x 4 experts, all loads issued at once
+    const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 3) / 4));
+    const int nj = H / kWave;
+    if (nj <= 16)
+      UOCR_LAUNCH("logits", k_logits_wide<16>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    else if (nj <= 20)
+      UOCR_LAUNCH("logits", k_logits_wide<20>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    else
+      UOCR_LAUNCH("logits", k_logits_wide<32>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    return hipGetLastError();
+  }
+  if (xb != nullptr) return hipErrorInvalidValue;
   if (T <= 8) {
     // decode: one wave per expert, every token of the step against it
-    const dim3 grid((E + 3) / 4, 1);
+    const dim3 grid((unsigned)((E + 3) / 4), 1);
     UOCR_LAUNCH("logits", (k_logits<8, 1>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
   } else {
-    const dim3 grid((E + 15) / 16, (T + 15) / 16);
+    const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16));
     UOCR_LAUNCH("logits", (k_logits<16, 4>), grid, dim3(256), 0, s, logits, x, ldx, router, T, E, H);
   }
   return hipGetLastError();

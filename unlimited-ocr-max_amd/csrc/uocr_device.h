@@ -144,6 +144,60 @@ __device__ __forceinline__ float wave_tree_sum(float v) {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// v of lane l + OFF for lanes l < OFF (OFF = 32, 16, 8, 4, 2, 1; other
+// lanes get values that are never used): v_permlane32/16_swap for the two
+// halving steps across 16-lane rows, DPP row_shl inside a row.  No LDS round
+// trip.
+template <int OFF>
+__device__ __forceinline__ uint32_t from_up(uint32_t v) {
+  if constexpr (OFF == 32) return __builtin_amdgcn_permlane32_swap(v, v, false, false)[1];
+  else if constexpr (OFF == 16) return __builtin_amdgcn_permlane16_swap(v, v, false, false)[1];
+  else return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + OFF, 0xf, 0xf, false);
+}
+template <int OFF>
+__device__ __forceinline__ float from_up(float v) { return __uint_as_float(from_up<OFF>(__float_as_uint(v))); }
+
+// Halving-tree sum over the 64 lanes, v[l] += v[l + off] for off = 32..1,
+// broadcast from lane 0 (the same additions, in the same order, as
+// wave_tree_sum).
+__device__ __forceinline__ float tree_sum(float v) {
+  v = v + from_up<32>(v);
+  v = v + from_up<16>(v);
+  v = v + from_up<8>(v);
+  v = v + from_up<4>(v);
+  v = v + from_up<2>(v);
+  v = v + from_up<1>(v);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ float tree_max(float v) {
+  v = fmaxf(v, from_up<32>(v));
+  v = fmaxf(v, from_up<16>(v));
+  v = fmaxf(v, from_up<8>(v));
+  v = fmaxf(v, from_up<4>(v));
+  v = fmaxf(v, from_up<2>(v));
+  v = fmaxf(v, from_up<1>(v));
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ uint32_t tree_umax(uint32_t v) {
+  v = max(v, from_up<32>(v));
+  v = max(v, from_up<16>(v));
+  v = max(v, from_up<8>(v));
+  v = max(v, from_up<4>(v));
+  v = max(v, from_up<2>(v));
+  v = max(v, from_up<1>(v));
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+__device__ __forceinline__ uint32_t tree_or(uint32_t v) {
+  v |= from_up<32>(v);
+  v |= from_up<16>(v);
+  v |= from_up<8>(v);
+  v |= from_up<4>(v);
+  v |= from_up<2>(v);
+  v |= from_up<1>(v);
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+
 __device__ __forceinline__ int clamp_expert(int32_t key, int E) {
   int e = key;
   e = e < 0 ? 0 : e;

@@ -77,9 +77,10 @@ hipError_t launch_gemv_pair(const GemvArgs& routed, int max_groups, const GemvAr
 
 // ---- routing (route.hip) ----
 
-// logits[t*E + e] = dot(x[t], router[e]) in the 64-lane tree order.
+// logits[t*E + e] = dot(x[t], router[e]) in the 64-lane tree order; xb (may
+// be null) receives x rounded to bf16, [T][H] (needs H % 64 == 0, H <= 2048).
 hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E,
-                         int H, hipStream_t s);
+                         int H, uint16_t* xb, hipStream_t s);
 // Softmax + top-k per token (one wave per token).  ids32/ids64/wts may be null.
 hipError_t launch_softmax_topk(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
                                int64_t* ids64, float* wts, hipStream_t s);
@@ -110,12 +111,13 @@ hipError_t launch_dequant(void* out, int out_f32, const int8_t* w, const float* 
                           int E, int N, int K, int groups, int vec, hipStream_t s);
 
 struct GemmProblem {
-  // A operand: rows of x (fp32, gathered) or h (bf16, packed in group order).
-  const float* x;        // fp32 activations [T, K] (gate/up)
-  int64_t ldx;
-  const uint16_t* hb;    // bf16 activations [rows, K] (down), used when x == null
-  int64_t ldh;
-  int x_div;             // activation row of routed row r is r / x_div
+  // A operand: bf16 rows [.., K] at a + row * lda; with grouped rows and
+  // a_by_token, row = group_rows[position] / x_div (gate/up: x rows), else
+  // row = position (down: h, already in group order; dense: the token).
+  const uint16_t* a;
+  int64_t lda;
+  int a_by_token;
+  int x_div;
   // B operand(s)
   Proj p[2];
   WKind kind;
@@ -132,7 +134,8 @@ struct GemmProblem {
   int64_t ldo;
   int out_by_position;        // 1: output row = position in group order, 0: row id
 };
-hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles,
+// bm: rows per tile, 64 or 128 (must match the group tables' tile_start).
+hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
                             hipStream_t s);
 
 // ---- the persistent decode layer (decode.hip) ----

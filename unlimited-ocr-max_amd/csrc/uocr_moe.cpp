@@ -18,8 +18,6 @@
 #include "uocr_kernels.h"
 
 namespace uocr {
-int gemm_bm();
-int gemm_bn();
 int gemm_bk();
 }  // namespace uocr
 
@@ -496,6 +494,7 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
 }
 
 struct PrefillBufs {
+  uint16_t* xb;  // x rounded to bf16 [T][H]
   float* logits;
   int32_t* ids;
   float* wts;
@@ -509,6 +508,7 @@ struct PrefillBufs {
 static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
   const int64_t R = T * L->top_k;
   PrefillBufs d{};
+  d.xb = c.take<uint16_t>(T * L->hidden);
   d.logits = c.take<float>(T * L->num_experts);
   d.ids = c.take<int32_t>(R);
   d.wts = c.take<float>(R);
@@ -545,7 +545,7 @@ int uocr_moe_gate(int64_t* indices, float* weights, const float* x, int64_t seq,
                         err, errlen))
     return 1;
   float* logits = static_cast<float*>(ws);
-  hipError_t e = launch_logits(logits, x, hidden, router, (int)seq, (int)num_experts, (int)hidden, s);
+  hipError_t e = launch_logits(logits, x, hidden, router, (int)seq, (int)num_experts, (int)hidden, nullptr, s);
   if (e == hipSuccess)
     e = launch_softmax_topk(logits, (int)seq, (int)num_experts, (int)top_k, renormalize, nullptr, indices, weights,
                             s);
@@ -602,7 +602,7 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
   const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
   const int max_groups = (int)(E < R ? E : R);
 
-  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)B, E, H, s);
+  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)B, E, H, nullptr, s);
   if (e == hipSuccess) e = launch_route_small(d.logits, (int)B, E, (int)L->top_k, L->renormalize, d.ids, d.wts, d.g, s);
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
 
@@ -697,10 +697,11 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
                      void* stream, char* err, size_t errlen) {
   const char* op = "uocr_moe_forward";
   if (check_layer(op, L, hidden, err, errlen)) return 1;
-  const int BN = gemm_bn(), BK = gemm_bk(), BM = gemm_bm();
-  if (L->hidden % BN || L->ffn % BN || L->shared_ffn % BN)
-    return fail(err, errlen, "%s: hidden, ffn and shared_ffn must be multiples of %d", op, BN);
-  if (L->int8 && L->group % BK) return fail(err, errlen, "%s: the int8 group must be a multiple of %d", op, BK);
+  const int BK = gemm_bk();
+  if (L->hidden % BK || L->ffn % BK || L->shared_ffn % BK)
+    return fail(err, errlen, "%s: hidden, ffn and shared_ffn must be multiples of %d", op, BK);
+  if (L->int8 && (L->group % 64 || BK % L->group != 0 && L->group % BK != 0))
+    return fail(err, errlen, "%s: the int8 group must be 64, 128 or a multiple of 128", op);
   if (!aligned16(x) || !aligned16(L->gate_proj) || !aligned16(L->up_proj) || !aligned16(L->down_proj) ||
       !aligned16(L->shared_gate) || !aligned16(L->shared_up) || !aligned16(L->shared_down))
     return fail(err, errlen, "%s: x and the weights must be 16-byte aligned", op);
@@ -708,6 +709,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   if (seq == 0) return 0;
   const hipStream_t s = (hipStream_t)stream;
   const int64_t T = seq, R = seq * L->top_k;
+  const int BM = R >= 8192 ? 128 : 64;  // rows per GEMM tile
   Carve dry(nullptr);
   carve_prefill(dry, L, T);
   void* ws = nullptr;
@@ -716,7 +718,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   const PrefillBufs d = carve_prefill(c, L, T);
   const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
 
-  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, s);
+  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s);
   if (e == hipSuccess)
     e = launch_softmax_topk(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, nullptr, d.wts, s);
   if (e == hipSuccess) e = launch_group(d.ids, (int)R, E, BM, d.g, s);
@@ -725,8 +727,9 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   const int max_mtiles = (int)((R + BM - 1) / BM) + max_groups;
 
   GemmProblem gu{};
-  gu.x = x;
-  gu.ldx = H;
+  gu.a = d.xb;
+  gu.lda = H;
+  gu.a_by_token = 1;
   gu.x_div = (int)L->top_k;
   gu.p[0] = Proj{L->gate_proj, L->gate_proj_scales};
   gu.p[1] = Proj{L->up_proj, L->up_proj_scales};
@@ -743,8 +746,9 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   gu.out_by_position = 1;
 
   GemmProblem sgu{};
-  sgu.x = x;
-  sgu.ldx = H;
+  sgu.a = d.xb;
+  sgu.lda = H;
+  sgu.a_by_token = 1;
   sgu.x_div = 1;
   sgu.p[0] = Proj{L->shared_gate, nullptr};
   sgu.p[1] = Proj{L->shared_up, nullptr};
@@ -756,13 +760,13 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sgu.swiglu = 1;
   sgu.outb = d.hsb;
   sgu.ldo = Fs;
-  e = launch_gemm_pair(gu, sgu, max_mtiles, s);
+  e = launch_gemm_pair(gu, sgu, BM, max_mtiles, s);
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
 
   GemmProblem dn = gu;
-  dn.x = nullptr;
-  dn.hb = d.hb;
-  dn.ldh = F;
+  dn.a = d.hb;
+  dn.lda = F;
+  dn.a_by_token = 0;
   dn.x_div = 1;
   dn.p[0] = Proj{L->down_proj, L->down_proj_scales};
   dn.p[1] = Proj{nullptr, nullptr};
@@ -775,9 +779,9 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   dn.ldo = H;
 
   GemmProblem sdn = sgu;
-  sdn.x = nullptr;
-  sdn.hb = d.hsb;
-  sdn.ldh = Fs;
+  sdn.a = d.hsb;
+  sdn.lda = Fs;
+  sdn.a_by_token = 0;
   sdn.p[0] = Proj{L->shared_down, nullptr};
   sdn.p[1] = Proj{nullptr, nullptr};
   sdn.N = H;
@@ -786,7 +790,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sdn.outb = nullptr;
   sdn.outf = d.sh;
   sdn.ldo = H;
-  e = launch_gemm_pair(dn, sdn, max_mtiles, s);
+  e = launch_gemm_pair(dn, sdn, BM, max_mtiles, s);
   if (e == hipSuccess) e = launch_combine(out, d.y, H, d.wts, d.g.inv, d.sh, (int)T, H, (int)L->top_k, s);
   if (e == hipSuccess && expert_ids) e = hipMemcpyAsync(expert_ids, d.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
   if (e == hipSuccess && expert_weights)
