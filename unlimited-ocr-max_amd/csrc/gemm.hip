@@ -156,44 +156,96 @@ struct StepRegs {
   float scale;
 };
 
+// Per-thread global cursors of a tile, set up once: the activation row, the
+// weight row (or K-blocked column run) and, for int8, the scale of the
+// thread's piece together with its position inside the quantisation group.
+struct Cursor {
+  const uint16_t* a;
+  const char* b;
+  const float* s;
+  int grem;   // K offset of the piece inside its group (groups wider than a step)
+  int gwrap;  // group width when wider than a step, else never reached
+  int sinc;   // scales per step when a step spans whole groups
+};
+
 template <int BM, WKind W, int NPROJ>
-__device__ __forceinline__ void load_step(const GemmProblem& P, const TileRef& t, const uint16_t* a_src, int k0,
-                                          StepRegs<BM, W>& R) {
+__device__ __forceinline__ Cursor make_cursor(const GemmProblem& P, const TileRef& t, const uint16_t* a_src) {
   using S = StepRegs<BM, W>;
   constexpr int T = S::kThreads;
   const int tid = (int)threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < S::kABytes / 16; ++i) R.a[i] = *(const UOCR_GLOBAL i32x4*)(a_src + k0 + 8 * i);
-  constexpr int NB = S::kBBytes / 16;
+  Cursor c;
+  c.a = a_src;
+  c.s = nullptr;
+  c.grem = 0;
+  c.gwrap = 0x7fffffff;
+  c.sinc = 0;
+  // the projection's pointers, selected without indexing the argument block
+  const void* w0 = P.p[0].w;
+  const void* w1 = NPROJ == 2 ? P.p[1].w : w0;
   if constexpr (W == kBf16KBlocked) {
-    // K-blocked [K/16][N][16]: 8 blocks x 256 rows x 32 bytes; thread -> block,
-    // consecutive rows (contiguous in memory)
+    // K-blocked [K/16][N][16]: 8 blocks x kBRows rows x 32 bytes per step;
+    // thread -> block, consecutive rows (contiguous in memory)
     constexpr int kRowsPer = kBRows * 8 / T;
     constexpr int kPerBlock = kBRows / kRowsPer;
     const int kb = tid / kPerBlock;
     const int r0 = (tid % kPerBlock) * kRowsPer;
     const int half = kBRows / NPROJ;
-    const int p = NPROJ == 2 ? r0 / half : 0;
+    const bool second = NPROJ == 2 && r0 >= half;
     const int n = t.n0 + (NPROJ == 2 ? r0 % half : r0);
-    const uint16_t* src = (const uint16_t*)P.p[p].w + ((int64_t)(k0 / 16 + kb) * P.N + n) * 16;
-#pragma unroll
-    for (int i = 0; i < NB; ++i) R.b[i] = *(const UOCR_GLOBAL i32x4*)(src + 8 * i);
+    c.b = (const char*)(second ? w1 : w0) + ((int64_t)kb * P.N + n) * 32;
   } else {
     constexpr int kParts = T / kBRows;  // threads per weight row
     const int row = tid / kParts;
     const int part = tid % kParts;
     const int half = kBRows / NPROJ;
-    const int p = NPROJ == 2 ? row / half : 0;
+    const bool second = NPROJ == 2 && row >= half;
     const int n = t.n0 + (NPROJ == 2 ? row % half : row);
     constexpr int kEsz = W == kInt8Rows ? 1 : 2;
-    const char* src =
-        (const char*)P.p[p].w + (((int64_t)t.e * P.N + n) * P.K + k0) * kEsz + part * S::kBBytes;
-#pragma unroll
-    for (int i = 0; i < NB; ++i) R.b[i] = *(const UOCR_GLOBAL i32x4*)(src + 16 * i);
+    c.b = (const char*)(second ? w1 : w0) + ((int64_t)t.e * P.N + n) * P.K * kEsz + part * S::kBBytes;
     if constexpr (W == kInt8Rows) {
+      const float* s0 = P.p[0].s;
+      const float* s1 = NPROJ == 2 ? P.p[1].s : s0;
+      // group widths are multiples of 64 that divide or are multiples of BK
       const int gsize = P.K / P.groups;
-      const int kk = k0 + part * S::kBBytes;
-      R.scale = ldg(P.p[p].s + ((int64_t)t.e * P.N + n) * P.groups + kk / gsize);
+      const int kk = part * S::kBBytes;
+      c.s = (second ? s1 : s0) + ((int64_t)t.e * P.N + n) * P.groups + kk / gsize;
+      if (gsize <= BK) {
+        c.sinc = BK / gsize;
+      } else {
+        c.gwrap = gsize;
+        c.grem = kk % gsize;
+      }
+    }
+  }
+  return c;
+}
+
+// Loads one K step at the cursor into registers.
+template <int BM, WKind W, int NPROJ>
+__device__ __forceinline__ void load_step(const Cursor& c, StepRegs<BM, W>& R) {
+  using S = StepRegs<BM, W>;
+#pragma unroll
+  for (int i = 0; i < S::kABytes / 16; ++i) R.a[i] = *(const UOCR_GLOBAL i32x4*)(c.a + 8 * i);
+  constexpr int NB = S::kBBytes / 16;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) R.b[i] = *(const UOCR_GLOBAL i32x4*)(c.b + 16 * i);
+  if constexpr (W == kInt8Rows) R.scale = ldg(c.s);
+}
+
+// Moves the cursor one K step on when `more` (else it stays on the last step,
+// whose data a repeated load finds in cache).
+template <WKind W>
+__device__ __forceinline__ void advance(const GemmProblem& P, Cursor& c, bool more) {
+  c.a += more ? BK : 0;
+  if constexpr (W == kBf16KBlocked) {
+    c.b += more ? (int64_t)8 * P.N * 32 : 0;  // the thread's K-block, 8 blocks on
+  } else {
+    c.b += more ? BK * (W == kInt8Rows ? 1 : 2) : 0;
+    if constexpr (W == kInt8Rows) {
+      const int grem = c.grem + (more ? BK : 0);
+      const bool wrap = grem >= c.gwrap;
+      c.s += (more ? c.sinc : 0) + (wrap ? 1 : 0);
+      c.grem = wrap ? grem - c.gwrap : grem;
     }
   }
 }
@@ -234,8 +286,8 @@ __device__ __forceinline__ void store_step(const StepRegs<BM, W>& R, uint16_t* A
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const int v = R.b[i][d];
-        o[2 * d] = pack_bf16x2((float)(int8_t)v * s, (float)(int8_t)(v >> 8) * s);
-        o[2 * d + 1] = pack_bf16x2((float)(int8_t)(v >> 16) * s, (float)(int8_t)(v >> 24) * s);
+        o[2 * d] = pack_bf16x2(i8_to_f32<0>(v) * s, i8_to_f32<1>(v) * s);
+        o[2 * d + 1] = pack_bf16x2(i8_to_f32<2>(v) * s, i8_to_f32<3>(v) * s);
       }
       dst[2 * i] = i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
       dst[2 * i + 1] = i32x4{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
@@ -259,6 +311,7 @@ __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds)
   const int a_row =
       (P.a_by_token && P.rows.n_groups != nullptr) ? ldg(P.rows.group_rows + a_pos) / P.x_div : a_pos;
   const uint16_t* a_src = P.a + (int64_t)a_row * P.lda + (tid % S::kAParts) * (S::kABytes / 2);
+  Cursor cur = make_cursor<BM, W, NPROJ>(P, t, a_src);
 
   f32x16 acc[2];
 #pragma unroll
@@ -269,14 +322,22 @@ __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds)
   const int brow0 = NPROJ == 2 ? wn * 32 : wn * 64;
   const int brow1 = NPROJ == 2 ? kBRows / 2 + wn * 32 : wn * 64 + 32;
 
+  // One K step of raw global data in flight: step ks + 1 is loaded into
+  // registers right after step ks has been stored from them, and lands while
+  // the matrix cores work on step ks (the barriers order LDS only, so they
+  // do not wait for it).
   S R;
-  load_step<BM, W, NPROJ>(P, t, a_src, 0, R);
   const int ksteps = P.K / BK;
+  load_step<BM, W, NPROJ>(cur, R);
+  advance<W>(P, cur, ksteps > 1);
   for (int ks = 0; ks < ksteps; ++ks) {
-    if (ks > 0) __syncthreads();
+    if (ks > 0) lds_barrier();
     store_step<BM, W>(R, As, Bs);
-    if (ks + 1 < ksteps) load_step<BM, W, NPROJ>(P, t, a_src, (ks + 1) * BK, R);
-    __syncthreads();
+    if (ks + 1 < ksteps) {
+      load_step<BM, W, NPROJ>(cur, R);
+      advance<W>(P, cur, ks + 2 < ksteps);
+    }
+    lds_barrier();
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       const int kofs = kk + (lane >> 5) * 8;
