@@ -312,6 +312,75 @@ def bench_cpu_baseline(layer_w, budget_s: float) -> dict:
     return out
 
 
+# ---------------------------------------------------------------------------- HBM traffic (rocprofv3 --pmc)
+
+COPY_ELEMS = 64 << 20  # the scale kernel: -x over 256 MiB of fp32 (reads 256 MiB, writes 256 MiB)
+
+
+def traffic_probe() -> int:
+    """Child mode run under ``rocprofv3 --pmc``: the int8 B=1 decode layer over the rotated layers (cold
+    HBM, as in the timed region), then an elementwise kernel of known size that scales the counter."""
+    import torch
+
+    dev = "cuda:0"
+    layers = [make_layer(1000 + l, True, dev)[0] for l in range(LAYERS)]
+    g = torch.Generator(device=dev).manual_seed(1)
+    xs = [rmsnorm_rows(g, 1, dev) for _ in range(LAYERS)]
+    ws = layers[0].workspace(1, prefill=False)
+    for i in range(2 * LAYERS):
+        layers[i % LAYERS].decode_rows(xs[i % LAYERS], workspace=ws)
+    src = torch.ones(COPY_ELEMS, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("traffic probe done", flush=True)
+    return 0
+
+
+def measure_traffic(kernel: str, timeout_s: int = 120) -> dict | None:
+    """HBM bytes per launch of ``kernel`` from two ``rocprofv3 --pmc`` passes (FETCH_SIZE, WRITE_SIZE) over
+    ``--traffic-probe``, each scaled so that the elementwise kernel reads and writes its known 256 MiB."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        log("traffic: rocprofv3 not found")
+        return None
+    res: dict = {}
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", counter, "--output-format", "csv",
+                   "-d", d, "-o", counter, "--", sys.executable, str(ROOT / "bench.py"), "--traffic-probe"]
+            log(f"traffic: {counter} pass")
+            r = subprocess.run(cmd, capture_output=True, text=True, env={**os.environ, "TMPDIR": "/tmp"})
+            if r.returncode != 0:
+                log(f"traffic: {counter} pass failed ({r.returncode}): {r.stderr[-400:]}")
+                return None
+            path = Path(d) / f"{counter}_counter_collection.csv"
+            per: dict[tuple[str, str], float] = {}
+            for row in csv.DictReader(open(path)):
+                if row["Counter_Name"] != counter:
+                    continue
+                key = (row["Dispatch_Id"], row["Kernel_Name"])
+                per[key] = per.get(key, 0.0) + float(row["Counter_Value"])
+            ours = [v for (_, n), v in per.items() if kernel in n]
+            scale = [v for (_, n), v in per.items() if "neg" in n]
+            if not ours or not scale:
+                log(f"traffic: {counter}: no dispatches of {kernel} or of the scale kernel")
+                return None
+            known_kib = COPY_ELEMS * 4 / 1024
+            factor = known_kib / statistics.mean(scale)
+            res[counter] = {"kib_per_launch": round(statistics.mean(ours), 1), "launches": len(ours),
+                            "scale_kernel_kib": round(statistics.mean(scale), 1), "factor": round(factor, 4)}
+    fetch = res["FETCH_SIZE"]["kib_per_launch"] * res["FETCH_SIZE"]["factor"] * 1024
+    write = res["WRITE_SIZE"]["kib_per_launch"] * res["WRITE_SIZE"]["factor"] * 1024
+    return {"bytes": int(fetch + write), "fetch_bytes": int(fetch), "write_bytes": int(write), "counters": res}
+
+
 # ---------------------------------------------------------------------------- main
 
 
@@ -323,7 +392,16 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline sampling")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="decode only (no prefill, no bf16)")
+    ap.add_argument("--batches", default="1,8", help="int8 decode batches to time (1 is required)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc traffic passes")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.traffic_probe:
+        return traffic_probe()
+    batches = sorted({int(b) for b in args.batches.split(",")})
+    if 1 not in batches:
+        print("--batches must include 1 (the headline workload)", file=sys.stderr)
+        return 2
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE block runs on a single MI355X here "
               "(run with --gpus 1; multi-GPU sharding is not part of this build)", file=sys.stderr)
@@ -347,12 +425,16 @@ def main() -> int:
     log("decode int8 B=1")
     results["decode_int8_b1"] = bench_decode(layers, 1, args.steps, args.warmup, True, dev, 1)
     log(f"  {results['decode_int8_b1']['us_per_layer']} us/layer")
-    log("decode int8 B=8")
-    results["decode_int8_b8"] = bench_decode(layers, 8, args.steps, args.warmup, True, dev, 8)
-    log(f"  {results['decode_int8_b8']['us_per_layer']} us/layer")
-    us8 = results["decode_int8_b8"]["us_per_layer"]
-    results["decode_int8_11layer_step_b8"] = {"us_per_step": round(11 * us8, 2),
-                                              "tokens_per_s": round(8 / (11 * us8 * 1e-6), 1)}
+    for B in batches:
+        if B == 1:
+            continue
+        log(f"decode int8 B={B}")
+        results[f"decode_int8_b{B}"] = bench_decode(layers, B, args.steps, args.warmup, True, dev, B)
+        log(f"  {results[f'decode_int8_b{B}']['us_per_layer']} us/layer")
+    if 8 in batches:
+        us8 = results["decode_int8_b8"]["us_per_layer"]
+        results["decode_int8_11layer_step_b8"] = {"us_per_step": round(11 * us8, 2),
+                                                  "tokens_per_s": round(8 / (11 * us8 * 1e-6), 1)}
     if not args.quick:
         log("prefill int8 T=512 (Zipf)")
         results["prefill_int8_t512"] = bench_prefill(layers_w, 512, dev, 512)
@@ -376,6 +458,11 @@ def main() -> int:
 
     b1 = results["decode_int8_b1"]
     fk = b1.get("fused_kernel", {})
+    traffic = None
+    if not args.no_traffic:
+        traffic = measure_traffic("k_decode_fused")
+        if traffic is not None:
+            results["traffic_decode_int8_b1"] = traffic
     line = {
         "metric": METRIC,
         "value": b1["us_per_layer"],
@@ -387,11 +474,12 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (int8 weights, fp32 activations and accumulation)",
+        "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "int8 MoE decode layer, batch 1, 11 seeded layers rotated (cold HBM), HIP graph",
                    "hidden": H, "moe_ffn": F, "routed_experts": E, "top_k": TOPK, "shared_ffn": FS,
-                   "group": GROUP, "batch": 1, "layers_rotated": LAYERS},
+                   "group": GROUP, "batch": 1, "layers_rotated": LAYERS,
+                   "operands": "int8 weights (fp32 per-128-group scales), fp32 activations and accumulation"},
         "roofline": {
             "bound": "hbm",
             "kernel": "decode_fused (the whole int8 MoE layer in one persistent kernel), decode B=1",
@@ -399,7 +487,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(fk["gbs"] / HBM_PEAK_GBS, 4) if fk else None,
-            "traffic": None,
+            "traffic": None if traffic is None else traffic["bytes"],
             "algorithmic_bytes_per_launch": fk.get("avg_bytes"),
             "avg_launch_us": fk.get("avg_us"),
         },
