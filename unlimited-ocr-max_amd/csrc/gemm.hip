@@ -295,6 +295,15 @@ __device__ __forceinline__ void store_step(const StepRegs<BM, W>& R, uint16_t* A
   }
 }
 
+// silu(g) * u for the prefill epilogue: v_exp_f32 and v_rcp_f32 (within a
+// couple of ulp of the correctly rounded value, far below the bf16 rounding
+// of h that follows; the prefill is held to a tolerance, the decode path
+// keeps its exactly specified silu).
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 template <int BM, WKind W, int NPROJ>
 __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds) {
   using S = StepRegs<BM, W>;
@@ -358,7 +367,7 @@ __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds)
     const int64_t orow = (int64_t)(t.pos0 + row);
     if constexpr (NPROJ == 2) {
       const int col = t.n0 + wn * 32 + (lane & 31);
-      stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(silu(acc[0][r]) * acc[1][r]));
+      stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(swiglu_fast(acc[0][r], acc[1][r])));
     } else {
       const int col = t.n0 + wn * 64 + (lane & 31);
       stg(P.outf + orow * P.ldo + col, acc[0][r]);
