@@ -74,6 +74,74 @@ __global__ void __launch_bounds__(256) k_logits_wide(float* __restrict__ logits,
   }
 }
 
+// logits[t][e] for TW tokens x EW experts per wave (grid: x = blocks of EW
+// experts, y = blocks of 4 TW tokens; the 4 waves of a workgroup share the
+// expert block, so its router rows come from L1 after the first wave), for
+// prefill sizes: every x row and router row is read T / TW + E / EW times
+// instead of once per (token, expert) quad.  Per lane the same fma chains over
+// k = lane + 64 j as k_logits_wide, the operands of step j + 1 loaded while
+// step j is computed, then the same 64-lane tree; the waves of the first
+// expert block also write the tokens' x rows rounded to bf16 (xb).
+template <int TW, int EW>
+__global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                                     const float* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ router, int T, int E, int H) {
+  const int w = (int)(threadIdx.x >> 6);
+  const int l = lane_id();
+  const int e0 = (int)blockIdx.x * EW;
+  const int t0 = ((int)blockIdx.y * 4 + w) * TW;
+  if (t0 >= T || e0 >= E) return;  // wave-uniform; the kernel has no barriers
+  const int nj = H / kWave;
+  const float* xl = x + (int64_t)t0 * ldx + l;
+  const float* wl = router + (int64_t)e0 * H + l;
+  int64_t xo[TW], wo[EW];  // wave-uniform row offsets (rows past the end repeat the last one)
+#pragma unroll
+  for (int t = 0; t < TW; ++t) xo[t] = (int64_t)min(t, T - 1 - t0) * ldx;
+#pragma unroll
+  for (int e = 0; e < EW; ++e) wo[e] = (int64_t)min(e, E - 1 - e0) * H;
+  const bool write_xb = xb != nullptr && blockIdx.x == 0;
+
+  float p[TW][EW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t)
+#pragma unroll
+    for (int e = 0; e < EW; ++e) p[t][e] = 0.0f;
+  float xa[TW], wa[EW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t) xa[t] = ldg(xl + xo[t]);
+#pragma unroll
+  for (int e = 0; e < EW; ++e) wa[e] = ldg(wl + wo[e]);
+#pragma unroll 2
+  for (int j = 0; j < nj; ++j) {
+    float xn[TW], wn[EW];
+    const int jn = min(j + 1, nj - 1) * kWave;
+#pragma unroll
+    for (int t = 0; t < TW; ++t) xn[t] = ldg(xl + xo[t] + jn);
+#pragma unroll
+    for (int e = 0; e < EW; ++e) wn[e] = ldg(wl + wo[e] + jn);
+    if (write_xb) {
+#pragma unroll
+      for (int t = 0; t < TW; ++t)
+        if (t0 + t < T) xb[(int64_t)(t0 + t) * H + l + j * kWave] = f32_to_bf16_rne(xa[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < TW; ++t)
+#pragma unroll
+      for (int e = 0; e < EW; ++e) p[t][e] = __builtin_fmaf(xa[t], wa[e], p[t][e]);
+#pragma unroll
+    for (int t = 0; t < TW; ++t) xa[t] = xn[t];
+#pragma unroll
+    for (int e = 0; e < EW; ++e) wa[e] = wn[e];
+  }
+#pragma unroll
+  for (int t = 0; t < TW; ++t)
+#pragma unroll
+    for (int e = 0; e < EW; ++e) {
+      const float v = tree_sum(p[t][e]);
+      if (l == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = v;
+    }
+}
+
 template <int TT, int EE>
 __global__ void __launch_bounds__(256) k_logits(float* __restrict__ logits, const float* __restrict__ x,
                                                 int64_t ldx, const float* __restrict__ router, int T, int E,
@@ -264,6 +332,16 @@ __global__ void __launch_bounds__(256) k_combine(float* __restrict__ out, const 
 hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E, int H,
                          uint16_t* xb, hipStream_t s) {
   if (T <= 0) return hipSuccess;
+  if (H % kWave == 0 && T >= 2048) {
+    const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 31) / 32));
+    UOCR_LAUNCH("logits", (k_logits_tile<8, 16>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    return hipGetLastError();
+  }
+  if (H % kWave == 0 && T >= 256) {
+    const dim3 grid((unsigned)((E + 7) / 8), (unsigned)((T + 15) / 16));
+    UOCR_LAUNCH("logits", (k_logits_tile<4, 8>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    return hipGetLastError();
+  }
   if (H % kWave == 0 && H <= kLogitsMaxH && (xb != nullptr || T > 8)) {
     // every wave: 4 tokens x 4 experts, all loads issued at once
     const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 3) / 4));
