@@ -182,6 +182,40 @@ def test_prefill_matches_float64(oracle, full_int8, full_bf16, which, T) -> None
     assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize(("int8", "group", "H", "F", "T"),
+                         [(True, 64, 384, 256, 40), (True, 256, 512, 256, 200), (False, 128, 384, 384, 130)],
+                         ids=["int8-G64-H384", "int8-G256-H512", "bf16-H384"])
+def test_prefill_small_shapes(oracle, int8, group, H, F, T) -> None:
+    """Column tiles that overhang N (down N = 384 against 256-column tiles), scale groups of 64 and 256, short
+    and partial row tiles."""
+    layer = oracle.make_layer(40 + H + group, E=8, H=H, F=F, n_shared=1, int8=int8, std=0.05, router_std=0.1,
+                              group=group)
+    moe = moe_for(layer)
+    x = oracle.rmsnorm_rows(np.random.default_rng(500 + T), T, H)
+    out, ids, wts = moe(t(x), routing=True)
+    ids_o, wts_o = oracle.moe_gate(x, layer.router, 6)
+    assert np.array_equal(n(ids), ids_o)
+    got = n(out)
+    ref = oracle.moe_layer_f64(x, layer, ids_o, wts_o, bf16_dequant=True)
+    rel = oracle.rel_err(got, ref)
+    print(f"[uocr] prefill small int8={int8} G={group} H={H} F={F} T={T}: rel {rel:.3e}")
+    assert rel <= 1e-2
+
+
+def test_prefill_128_row_tiles(oracle, full_int8) -> None:
+    """T = 2048 (12288 routed rows): the launch runs 128-row tiles."""
+    moe = moe_for(full_int8)
+    x = oracle.rmsnorm_rows(np.random.default_rng(2048), 2048, 1280)
+    out, ids, wts = moe(t(x), routing=True)
+    ids_o, wts_o = oracle.moe_gate(x, full_int8.router, 6)
+    assert np.array_equal(n(ids), ids_o)
+    got = n(out)
+    ref = oracle.moe_layer_f64(x, full_int8, ids_o, wts_o, bf16_dequant=True)
+    rel = oracle.rel_err(got, ref)
+    print(f"[uocr] prefill int8 T=2048: rel {rel:.3e}")
+    assert rel <= 1e-2
+
+
 def test_prefill_adversarial_routing(oracle, full_int8) -> None:
     """Router logits +10 on experts 0-5 for every token: six groups of all T tokens."""
     import dataclasses

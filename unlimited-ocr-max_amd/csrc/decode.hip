@@ -453,6 +453,7 @@ struct Ctx {
 // before the x rows are staged, then every token's logit in the 64-lane tree
 // order, stored into each copy of the logits.
 constexpr int kMaxJ = 32;  // H <= 2048
+constexpr int kRouterWaves = 4;  // router tasks per workgroup (E = 64: the first 16 workgroups)
 
 __device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A, int e, float (&w)[kMaxJ]) {
   const int l = lane();
@@ -766,11 +767,18 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   C.tag = epoch + 1u;
   const int nwaves = (int)gridDim.x * kWaves;
   const int rank = wave * (int)gridDim.x + (int)blockIdx.x;
-  int t = rank;
+  // Router task e runs on wave e % 4 of workgroup e / 4: workgroups that
+  // start early (the grid's start is spread over about a microsecond, and
+  // every routing waits for the last logit), few enough router rows per CU
+  // that their loads do not queue behind each other.  Every wave then takes
+  // the rest of the task list from E + rank on.
+  const int re = (int)blockIdx.x * kRouterWaves + wave;
+  const bool router = wave < kRouterWaves && re < A.E;
+  int t = A.E + rank;
 
   // a router task's weights do not depend on x: they load while x is staged
   float w[kMaxJ];
-  if (t < A.E) router_load(A, t, w);
+  if (router) router_load(A, re, w);
 
   // x rows into LDS, each 128-element chunk padded to kXPad floats
   for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
@@ -782,13 +790,12 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(A.ctl + C_ARRIVED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  for (bool first = true; t < A.E; t += nwaves, first = false) {
-    C.t = t;
-    UOCR_TRACE(A, t, 0);
-    if (!first) router_load(A, t, w);
-    router_task(A, C, t, w);
-    UOCR_TRACE(A, t, 2);
-    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 7] = rank;
+  if (router) {
+    C.t = re;
+    UOCR_TRACE(A, re, 0);
+    router_task(A, C, re, w);
+    UOCR_TRACE(A, re, 2);
+    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)re * 8 + 7] = rank;
   }
   // The routing of token i is computed by wave kWaves-1-i (high waves, whose
   // tasks come late in the list); the other waves meanwhile run their tasks
@@ -870,6 +877,8 @@ hipError_t fused_grid(size_t lds_bytes, int* grid) {
 }
 
 hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+  // every router task needs its workgroup (the routing waits for all logits)
+  if ((int64_t)grid * kRouterWaves < a.E) return hipErrorInvalidConfiguration;
   UOCR_LAUNCH("decode_fused", k_decode_fused, dim3(grid), dim3(kThreads), lds_bytes, s, a);
   return hipGetLastError();
 }

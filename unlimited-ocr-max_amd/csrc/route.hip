@@ -26,10 +26,19 @@ namespace {
 // when asked: the prefill GEMM's A operand.
 constexpr int kLogitsMaxH = 2048;
 
+// The first workgroup of a launch clears `n` words for a later kernel of the
+// same stream (the routing's counters).
+__device__ __forceinline__ void zero_words_once(int32_t* p, int n) {
+  if (p != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = (int)threadIdx.x; i < n; i += (int)blockDim.x) p[i] = 0;
+}
+
 template <int kJ>  // >= H / 64
 __global__ void __launch_bounds__(256) k_logits_wide(float* __restrict__ logits, uint16_t* __restrict__ xb,
                                                      const float* __restrict__ x, int64_t ldx,
-                                                     const float* __restrict__ router, int T, int E, int H) {
+                                                     const float* __restrict__ router, int T, int E, int H,
+                                                     int32_t* __restrict__ zero, int nzero) {
+  zero_words_once(zero, nzero);
   const int w = (int)(threadIdx.x >> 6);
   const int l = lane_id();
   const int e0 = (int)blockIdx.x * 16 + w * 4;
@@ -85,7 +94,9 @@ __global__ void __launch_bounds__(256) k_logits_wide(float* __restrict__ logits,
 template <int TW, int EW>
 __global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits, uint16_t* __restrict__ xb,
                                                      const float* __restrict__ x, int64_t ldx,
-                                                     const float* __restrict__ router, int T, int E, int H) {
+                                                     const float* __restrict__ router, int T, int E, int H,
+                                                     int32_t* __restrict__ zero, int nzero) {
+  zero_words_once(zero, nzero);
   const int w = (int)(threadIdx.x >> 6);
   const int l = lane_id();
   const int e0 = (int)blockIdx.x * EW;
@@ -251,55 +262,236 @@ __global__ void __launch_bounds__(256) k_softmax_topk(const float* __restrict__ 
 
 constexpr int kMaxGroupExperts = 1024;
 
-// Groups R rows by clamped expert id; `idof(r)` returns row r's raw id.
-// Counts are exact; within a group the row order is whatever the LDS atomics
-// give, which no output depends on (each row is computed on its own).
+// Lanes of the wave whose key equals this lane's (keys < 2^bits): one ballot
+// per key bit.
+__device__ __forceinline__ uint64_t same_key_lanes(int key, int bits) {
+  uint64_t m = ~0ull;
+  for (int b = 0; b < bits; ++b) {
+    const int bit = (key >> b) & 1;
+    const uint64_t on = __ballot(bit);
+    m &= bit ? on : ~on;
+  }
+  return m;
+}
+
+// Set bits of m below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int u = __shfl_up(v, d);
+    if (l >= d) v += u;
+  }
+  return v;
+}
+
+// Groups R rows by clamped expert id, stably: a group holds its rows in row
+// order.  `idof(r)` returns row r's raw id.  One workgroup of up to 16 waves
+// and E <= blockDim.x; `hist` is LDS of (waves x E) ints, `part` of 3 x 16.
+//
+// Wave w owns the rows [w * chunk, (w + 1) * chunk).  Pass 1 counts its rows
+// per expert, 64 rows at a time: the lanes holding one expert find each other
+// with one ballot per key bit, and the lowest of them adds their number.  The
+// counts are turned into each wave's first position per expert (experts in
+// order, waves in order inside an expert), and pass 2 walks the same rows
+// again, placing each at its wave's cursor plus its rank among the batch's
+// lanes of the same expert.  No atomics, and the order is fixed.
 template <typename IdOf>
-__device__ void group_rows(IdOf idof, int R, int E, int bm, const GroupTables& g, int* cnt, int* cursor) {
+__device__ void group_rows(IdOf idof, int R, int E, int bm, const GroupTables& g, int* hist, int* part) {
   const int tid = (int)threadIdx.x;
   const int nt = (int)blockDim.x;
-  for (int e = tid; e < E; e += nt) cnt[e] = 0;
+  const int nw = nt / kWave;
+  const int w = tid / kWave;
+  const int bits = 32 - __builtin_clz((unsigned)E);  // key E (no row) fits too
+  for (int i = tid; i < nw * E; i += nt) hist[i] = 0;
   __syncthreads();
-  for (int r = tid; r < R; r += nt) atomicAdd(&cnt[clamp_expert(idof(r), E)], 1);
-  __syncthreads();
-  if (tid == 0) {
-    int off = 0, ng = 0, tiles = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = cnt[e];
-      cursor[e] = off;
-      if (c > 0) {
-        stg(g.group_expert + ng, e);
-        stg(g.group_start + ng, off);
-        if (g.tile_start) stg(g.tile_start + ng, tiles);
-        tiles += (c + bm - 1) / bm;
-        ++ng;
-      }
-      off += c;
-    }
-    stg(g.group_start + ng, off);
-    if (g.tile_start) stg(g.tile_start + ng, tiles);
-    stg(g.n_groups, ng);
+  const int chunk = ((R + nw - 1) / nw + kWave - 1) / kWave * kWave;
+  const int r0 = w * chunk;
+  const int r1 = min(R, r0 + chunk);
+  int* my = hist + w * E;
+  for (int b = r0; b < r1; b += kWave) {
+    const int r = b + lane_id();
+    const int e = r < r1 ? clamp_expert(idof(r), E) : E;
+    const uint64_t m = same_key_lanes(e, bits);
+    if (e < E && lanes_below(m) == 0) my[e] += __popcll(m);
   }
   __syncthreads();
-  for (int r = tid; r < R; r += nt) {
-    const int pos = atomicAdd(&cursor[clamp_expert(idof(r), E)], 1);
-    stg(g.group_rows + pos, r);
-    if (g.inv) stg(g.inv + r, pos);
+
+  // per expert: rows, row tiles and whether it is a group; exclusive prefix
+  // sums over the experts (per wave, then across the waves' totals)
+  int c = 0;
+  if (tid < E) {
+    for (int v = 0; v < nw; ++v) {
+      const int h = hist[v * E + tid];
+      hist[v * E + tid] = c;
+      c += h;
+    }
+  }
+  const int tiles = c > 0 ? (c + bm - 1) / bm : 0;
+  const int nz = c > 0 ? 1 : 0;
+  const int ic = wave_inclusive_sum(c), it = wave_inclusive_sum(tiles), in = wave_inclusive_sum(nz);
+  if (lane_id() == kWave - 1) {
+    part[w] = ic;
+    part[16 + w] = it;
+    part[32 + w] = in;
+  }
+  __syncthreads();
+  int pc = 0, pt = 0, pn = 0;
+  for (int v = 0; v < w; ++v) {
+    pc += part[v];
+    pt += part[16 + v];
+    pn += part[32 + v];
+  }
+  const int start = pc + ic - c, tile0 = pt + it - tiles, grp = pn + in - nz;
+  if (tid < E) {
+    if (c > 0) {
+      stg(g.group_expert + grp, tid);
+      stg(g.group_start + grp, start);
+      if (g.tile_start) stg(g.tile_start + grp, tile0);
+    }
+    for (int v = 0; v < nw; ++v) hist[v * E + tid] += start;
+    if (tid == E - 1) {
+      stg(g.group_start + grp + nz, start + c);
+      if (g.tile_start) stg(g.tile_start + grp + nz, tile0 + tiles);
+      stg(g.n_groups, grp + nz);
+    }
+  }
+  __syncthreads();
+
+  for (int b = r0; b < r1; b += kWave) {
+    const int r = b + lane_id();
+    const int e = r < r1 ? clamp_expert(idof(r), E) : E;
+    const uint64_t m = same_key_lanes(e, bits);
+    const int rank = lanes_below(m);
+    const int base = e < E ? my[e] : 0;
+    if (e < E) {
+      const int pos = base + rank;
+      stg(g.group_rows + pos, r);
+      if (g.inv) stg(g.inv + r, pos);
+      if (rank == 0) my[e] = base + __popcll(m);
+    }
   }
 }
 
+// LDS of group_rows for a workgroup of `threads` threads.
+__host__ __device__ constexpr size_t group_lds_bytes(int threads, int E) {
+  return ((size_t)(threads / 64) * E + 48) * sizeof(int);
+}
+
 __global__ void __launch_bounds__(1024) k_group(const int32_t* __restrict__ ids, int R, int E, int bm, GroupTables g) {
-  __shared__ int cnt[kMaxGroupExperts];
-  __shared__ int cursor[kMaxGroupExperts];
-  group_rows([&](int r) { return ids[r]; }, R, E, bm, g, cnt, cursor);
+  extern __shared__ int lds_group[];
+  group_rows([&](int r) { return ids[r]; }, R, E, bm, g, lds_group + 48, lds_group);
+}
+
+// ---------------------------------------------------------------- prefill routing over many workgroups
+//
+// k_topk_count: a wave per token (softmax + top-k), 16 tokens per workgroup;
+// the workgroup counts its rows per expert and reserves that many places of
+// each expert with one atomic add on the expert's row total (cleared by the
+// logits launch), keeping the returned offset.  k_group_scatter: from the
+// totals, every workgroup derives the groups and row tiles (workgroup 0
+// writes those tables) and places the rows of kScatterSpan counting
+// workgroups at their reserved offsets.  Within one counting workgroup's
+// rows of an expert, and between counting workgroups, the order is the
+// atomics' (each row is computed on its own, so nothing depends on it).
+
+constexpr int kCountThreads = 1024;
+constexpr int kCountTokens = kCountThreads / 64;
+constexpr int kScatterThreads = 256;
+constexpr int kScatterSpan = 1;  // counting workgroups per scatter workgroup
+
+__global__ void __launch_bounds__(kCountThreads) k_topk_count(const float* __restrict__ logits, int T, int E, int topk,
+                                                              int renorm, int32_t* __restrict__ ids32,
+                                                              float* __restrict__ wts, int32_t* __restrict__ total,
+                                                              int32_t* __restrict__ base) {
+  __shared__ int cnt[kRouteMaxExperts];
+  const int b = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  const int t0 = b * kCountTokens;
+  const int t1 = min(T, t0 + kCountTokens);
+  for (int e = tid; e < E; e += kCountThreads) cnt[e] = 0;
+  const int t = t0 + tid / kWave;
+  if (t < t1) {
+    const int64_t o = (int64_t)t * topk;
+    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, nullptr);
+  }
+  __syncthreads();  // the block's ids (global) are visible to the whole workgroup
+  for (int64_t r = (int64_t)t0 * topk + tid; r < (int64_t)t1 * topk; r += kCountThreads)
+    atomicAdd(&cnt[clamp_expert(ids32[r], E)], 1);
+  __syncthreads();
+  for (int e = tid; e < E; e += kCountThreads) {
+    const int c = cnt[e];
+    if (c > 0) stg(base + (int64_t)b * E + e, atomicAdd(total + e, c));
+  }
+}
+
+__global__ void __launch_bounds__(kScatterThreads) k_group_scatter(const int32_t* __restrict__ ids, int T, int E,
+                                                                   int topk, int bm, const int32_t* __restrict__ total,
+                                                                   const int32_t* __restrict__ base, GroupTables g) {
+  __shared__ int cursor[kRouteMaxExperts];
+  __shared__ int start_of[kRouteMaxExperts];
+  __shared__ int part[12];
+  const int tid = (int)threadIdx.x;
+  const int w = tid / kWave;
+  const int tot = tid < E ? ldg(total + tid) : 0;
+  const int tiles = tot > 0 ? (tot + bm - 1) / bm : 0;
+  const int nz = tot > 0 ? 1 : 0;
+  const int ic = wave_inclusive_sum(tot), it = wave_inclusive_sum(tiles), in = wave_inclusive_sum(nz);
+  if (lane_id() == kWave - 1) {
+    part[w] = ic;
+    part[4 + w] = it;
+    part[8 + w] = in;
+  }
+  __syncthreads();
+  int pc = 0, pt = 0, pn = 0;
+  for (int v = 0; v < w; ++v) {
+    pc += part[v];
+    pt += part[4 + v];
+    pn += part[8 + v];
+  }
+  const int start = pc + ic - tot, tile0 = pt + it - tiles, grp = pn + in - nz;
+  if (tid < E) {
+    start_of[tid] = start;
+    if (blockIdx.x == 0) {
+      if (tot > 0) {
+        stg(g.group_expert + grp, tid);
+        stg(g.group_start + grp, start);
+        if (g.tile_start) stg(g.tile_start + grp, tile0);
+      }
+      if (tid == E - 1) {
+        stg(g.group_start + grp + nz, start + tot);
+        if (g.tile_start) stg(g.tile_start + grp + nz, tile0 + tiles);
+        stg(g.n_groups, grp + nz);
+      }
+    }
+  }
+  const int nblocks = (T + kCountTokens - 1) / kCountTokens;
+  const int b0 = (int)blockIdx.x * kScatterSpan;
+  const int b1 = min(nblocks, b0 + kScatterSpan);
+  for (int b = b0; b < b1; ++b) {
+    __syncthreads();  // start_of is written; the previous block's cursors are done
+    // (offsets of experts with no row in block b are stale and never read)
+    if (tid < E) cursor[tid] = start_of[tid] + ldg(base + (int64_t)b * E + tid);
+    __syncthreads();
+    const int64_t r0 = (int64_t)b * kCountTokens * topk;
+    const int64_t r1 = min((int64_t)T * topk, r0 + (int64_t)kCountTokens * topk);
+    for (int64_t r = r0 + tid; r < r1; r += kScatterThreads) {
+      const int pos = atomicAdd(&cursor[clamp_expert(ldg(ids + r), E)], 1);
+      stg(g.group_rows + pos, (int32_t)r);
+      if (g.inv) stg(g.inv + r, pos);
+    }
+  }
 }
 
 constexpr int kSmallTokens = 64;
 
 __global__ void __launch_bounds__(1024) k_route_small(const float* __restrict__ logits, int T, int E, int topk,
                                                       int renorm, int32_t* ids32, float* wts, GroupTables g) {
-  __shared__ int cnt[kMaxGroupExperts];
-  __shared__ int cursor[kMaxGroupExperts];
+  extern __shared__ int lds_group[];
   __shared__ int ids_lds[kSmallTokens * 64];
   const int nw = (int)(blockDim.x >> 6);
   for (int t = (int)(threadIdx.x >> 6); t < T; t += nw) {
@@ -307,39 +499,67 @@ __global__ void __launch_bounds__(1024) k_route_small(const float* __restrict__ 
     token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + o);
   }
   __syncthreads();
-  group_rows([&](int r) { return ids_lds[r]; }, T * topk, E, 1, g, cnt, cursor);
+  group_rows([&](int r) { return ids_lds[r]; }, T * topk, E, 1, g, lds_group + 48, lds_group);
 }
 
 // ---------------------------------------------------------------- combine
 
-__global__ void __launch_bounds__(256) k_combine(float* __restrict__ out, const float* __restrict__ y, int64_t ldy,
-                                                 const float* __restrict__ wts, const int32_t* __restrict__ inv,
-                                                 const float* __restrict__ shared, int T, int H, int topk) {
-  const int t = (int)blockIdx.y;
-  const int n = (int)blockIdx.x * 256 + (int)threadIdx.x;
-  if (n >= H) return;
-  float acc = 0.0f;
-  for (int j = 0; j < topk; ++j) {
-    const int i = t * topk + j;
-    const int row = inv ? inv[i] : i;
-    acc = __builtin_fmaf(wts[i], y[(int64_t)row * ldy + n], acc);
+constexpr int kCombineThreads = 320;  // 1280 columns as float4
+constexpr int kCombineMaxK = 8;  // rows loaded per round
+
+// A workgroup per token; a thread takes W = 4 consecutive columns (16-byte
+// loads, when every row and `out` are 16-byte aligned) or W = 1.
+template <int W>
+__global__ void __launch_bounds__(kCombineThreads) k_combine(float* __restrict__ out, const float* __restrict__ y,
+                                                             int64_t ldy, const float* __restrict__ wts,
+                                                             const int32_t* __restrict__ inv,
+                                                             const float* __restrict__ shared, int T, int H, int topk) {
+  typedef float vec __attribute__((ext_vector_type(W)));
+  const int t = (int)blockIdx.x;
+  for (int n = W * (int)threadIdx.x; n < H; n += W * kCombineThreads) {
+    vec acc = {};
+    // up to kCombineMaxK rows in flight; the fma chain stays in slot order
+    for (int j0 = 0; j0 < topk; j0 += kCombineMaxK) {
+      vec v[kCombineMaxK];
+#pragma unroll
+      for (int j = 0; j < kCombineMaxK; ++j) {
+        if (j0 + j < topk) {
+          const int i = t * topk + j0 + j;
+          const int row = inv ? ldc(inv + i) : i;
+          v[j] = *(const UOCR_GLOBAL vec*)(y + (int64_t)row * ldy + n);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kCombineMaxK; ++j) {
+        if (j0 + j < topk) {
+          const float wj = ldc(wts + t * topk + j0 + j);
+#pragma unroll
+          for (int c = 0; c < W; ++c) acc[c] = __builtin_fmaf(wj, v[j][c], acc[c]);
+        }
+      }
+    }
+    if (shared) {
+      const vec sh = *(const UOCR_GLOBAL vec*)(shared + (int64_t)t * H + n);
+#pragma unroll
+      for (int c = 0; c < W; ++c) acc[c] = acc[c] + sh[c];
+    }
+    *(UOCR_GLOBAL vec*)(out + (int64_t)t * H + n) = acc;
   }
-  out[(int64_t)t * H + n] = shared ? acc + shared[(int64_t)t * H + n] : acc;
 }
 
 }  // namespace
 
 hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E, int H,
-                         uint16_t* xb, hipStream_t s) {
+                         uint16_t* xb, hipStream_t s, int32_t* zero, int nzero) {
   if (T <= 0) return hipSuccess;
   if (H % kWave == 0 && T >= 2048) {
     const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 31) / 32));
-    UOCR_LAUNCH("logits", (k_logits_tile<8, 16>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    UOCR_LAUNCH("logits", (k_logits_tile<8, 16>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H, zero, nzero);
     return hipGetLastError();
   }
   if (H % kWave == 0 && T >= 256) {
     const dim3 grid((unsigned)((E + 7) / 8), (unsigned)((T + 15) / 16));
-    UOCR_LAUNCH("logits", (k_logits_tile<4, 8>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+    UOCR_LAUNCH("logits", (k_logits_tile<4, 8>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H, zero, nzero);
     return hipGetLastError();
   }
   if (H % kWave == 0 && H <= kLogitsMaxH && (xb != nullptr || T > 8)) {
@@ -347,14 +567,14 @@ hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float
     const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 3) / 4));
     const int nj = H / kWave;
     if (nj <= 16)
-      UOCR_LAUNCH("logits", k_logits_wide<16>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+      UOCR_LAUNCH("logits", k_logits_wide<16>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H, zero, nzero);
     else if (nj <= 20)
-      UOCR_LAUNCH("logits", k_logits_wide<20>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+      UOCR_LAUNCH("logits", k_logits_wide<20>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H, zero, nzero);
     else
-      UOCR_LAUNCH("logits", k_logits_wide<32>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H);
+      UOCR_LAUNCH("logits", k_logits_wide<32>, grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H, zero, nzero);
     return hipGetLastError();
   }
-  if (xb != nullptr) return hipErrorInvalidValue;
+  if (xb != nullptr || zero != nullptr) return hipErrorInvalidValue;
   if (T <= 8) {
     // decode: one wave per expert, every token of the step against it
     const dim3 grid((unsigned)((E + 3) / 4), 1);
@@ -376,21 +596,42 @@ hipError_t launch_softmax_topk(const float* logits, int T, int E, int topk, int 
 
 hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s) {
   if (E > kMaxGroupExperts) return hipErrorInvalidValue;
-  UOCR_LAUNCH("group", k_group, dim3(1), dim3(1024), 0, s, ids, R, E, bm, g);
+  UOCR_LAUNCH("group", k_group, dim3(1), dim3(1024), group_lds_bytes(1024, E), s, ids, R, E, bm, g);
+  return hipGetLastError();
+}
+
+int route_count_blocks(int T) { return (T + kCountTokens - 1) / kCountTokens; }
+
+hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
+                             int bm, const GroupTables& g, int32_t* total, int32_t* base, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (E > kRouteMaxExperts || E > kScatterThreads) return hipErrorInvalidValue;
+  const int blocks = route_count_blocks(T);
+  UOCR_LAUNCH("topk_count", k_topk_count, dim3(blocks), dim3(kCountThreads), 0, s, logits, T, E, topk, renorm, ids32,
+              wts, total, base);
+  UOCR_LAUNCH("group_scatter", k_group_scatter, dim3((blocks + kScatterSpan - 1) / kScatterSpan),
+              dim3(kScatterThreads), 0, s, ids32, T, E, topk, bm, total, base, g);
   return hipGetLastError();
 }
 
 hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
                               const GroupTables& g, hipStream_t s) {
   if (T > kSmallTokens || E > 64 || topk > 64) return hipErrorInvalidValue;
-  UOCR_LAUNCH("route_small", k_route_small, dim3(1), dim3(1024), 0, s, logits, T, E, topk, renorm, ids32, wts, g);
+  UOCR_LAUNCH("route_small", k_route_small, dim3(1), dim3(1024), group_lds_bytes(1024, E), s, logits, T, E, topk,
+              renorm, ids32, wts, g);
   return hipGetLastError();
 }
 
 hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* wts, const int32_t* inv,
                           const float* shared, int T, int H, int topk, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  UOCR_LAUNCH("combine", k_combine, dim3((H + 255) / 256, T), dim3(256), 0, s, out, y, ldy, wts, inv, shared, T, H, topk);
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (H % 4 == 0 && ldy % 4 == 0 && a16(out) && a16(y) && (shared == nullptr || a16(shared)))
+    UOCR_LAUNCH("combine", k_combine<4>, dim3(T), dim3(kCombineThreads), 0, s, out, y, ldy, wts, inv, shared, T, H,
+                topk);
+  else
+    UOCR_LAUNCH("combine", k_combine<1>, dim3(T), dim3(kCombineThreads), 0, s, out, y, ldy, wts, inv, shared, T, H,
+                topk);
   return hipGetLastError();
 }
 

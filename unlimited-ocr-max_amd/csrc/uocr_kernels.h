@@ -79,8 +79,9 @@ hipError_t launch_gemv_pair(const GemvArgs& routed, int max_groups, const GemvAr
 
 // logits[t*E + e] = dot(x[t], router[e]) in the 64-lane tree order; xb (may
 // be null) receives x rounded to bf16, [T][H] (needs H % 64 == 0, H <= 2048).
+// zero (may be null): nzero words the launch clears for a later kernel.
 hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E,
-                         int H, uint16_t* xb, hipStream_t s);
+                         int H, uint16_t* xb, hipStream_t s, int32_t* zero = nullptr, int nzero = 0);
 // Softmax + top-k per token (one wave per token).  ids32/ids64/wts may be null.
 hipError_t launch_softmax_topk(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
                                int64_t* ids64, float* wts, hipStream_t s);
@@ -95,6 +96,14 @@ struct GroupTables {
 };
 // Groups R rows by their clamped expert id (ascending expert).
 hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s);
+// Prefill routing over many workgroups (E <= 256): softmax + top-k of T
+// tokens, then the grouping of their T*topk rows.  `total` (E ints) must be
+// zero when the first kernel starts (launch_logits clears it); `base` holds
+// route_count_blocks(T) * E ints of scratch.
+constexpr int kRouteMaxExperts = 256;
+int route_count_blocks(int T);
+hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
+                             int bm, const GroupTables& g, int32_t* total, int32_t* base, hipStream_t s);
 // Decode-size routing in one workgroup: softmax + top-k of T <= 64 tokens, then
 // the grouping of their T*topk rows.
 hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,

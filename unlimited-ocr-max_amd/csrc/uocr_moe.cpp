@@ -503,6 +503,8 @@ struct PrefillBufs {
   uint16_t* hsb;
   float* y;
   float* sh;
+  int32_t* total;  // rows per expert (routing counters)
+  int32_t* base;   // per counting workgroup: its first place per expert
 };
 
 static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
@@ -517,6 +519,8 @@ static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
   d.hsb = c.take<uint16_t>(T * L->shared_ffn);
   d.y = c.take<float>(R * L->hidden);
   d.sh = c.take<float>(T * L->hidden);
+  d.total = c.take<int32_t>(L->num_experts);
+  d.base = c.take<int32_t>((int64_t)route_count_blocks((int)T) * L->num_experts);
   return d;
 }
 
@@ -718,10 +722,15 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   const PrefillBufs d = carve_prefill(c, L, T);
   const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
 
-  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s);
-  if (e == hipSuccess)
+  const bool many = E <= kRouteMaxExperts;
+  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s, many ? d.total : nullptr, E);
+  if (e == hipSuccess && many) {
+    e = launch_topk_group(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, d.wts, BM, d.g, d.total, d.base,
+                          s);
+  } else if (e == hipSuccess) {
     e = launch_softmax_topk(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, nullptr, d.wts, s);
-  if (e == hipSuccess) e = launch_group(d.ids, (int)R, E, BM, d.g, s);
+    if (e == hipSuccess) e = launch_group(d.ids, (int)R, E, BM, d.g, s);
+  }
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
   const int max_groups = (int)(E < R ? E : R);
   const int max_mtiles = (int)((R + BM - 1) / BM) + max_groups;
