@@ -117,32 +117,33 @@ __global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits,
   for (int t = 0; t < TW; ++t)
 #pragma unroll
     for (int e = 0; e < EW; ++e) p[t][e] = 0.0f;
-  float xa[TW], wa[EW];
+  // JB steps of x and router values are requested at once (one memory
+  // latency per JB steps); each lane's chain still runs over j in order
+  constexpr int JB = TW * EW >= 128 ? 2 : 5;
+  for (int j0 = 0; j0 < nj; j0 += JB) {
+    float xa[JB][TW], wa[JB][EW];
 #pragma unroll
-  for (int t = 0; t < TW; ++t) xa[t] = ldg(xl + xo[t]);
+    for (int jj = 0; jj < JB; ++jj) {
+      const int jo = min(j0 + jj, nj - 1) * kWave;
 #pragma unroll
-  for (int e = 0; e < EW; ++e) wa[e] = ldg(wl + wo[e]);
-#pragma unroll 2
-  for (int j = 0; j < nj; ++j) {
-    float xn[TW], wn[EW];
-    const int jn = min(j + 1, nj - 1) * kWave;
+      for (int t = 0; t < TW; ++t) xa[jj][t] = ldg(xl + xo[t] + jo);
 #pragma unroll
-    for (int t = 0; t < TW; ++t) xn[t] = ldg(xl + xo[t] + jn);
-#pragma unroll
-    for (int e = 0; e < EW; ++e) wn[e] = ldg(wl + wo[e] + jn);
-    if (write_xb) {
-#pragma unroll
-      for (int t = 0; t < TW; ++t)
-        if (t0 + t < T) xb[(int64_t)(t0 + t) * H + l + j * kWave] = f32_to_bf16_rne(xa[t]);
+      for (int e = 0; e < EW; ++e) wa[jj][e] = ldg(wl + wo[e] + jo);
     }
 #pragma unroll
-    for (int t = 0; t < TW; ++t)
+    for (int jj = 0; jj < JB; ++jj) {
+      if (j0 + jj < nj) {
+        if (write_xb) {
 #pragma unroll
-      for (int e = 0; e < EW; ++e) p[t][e] = __builtin_fmaf(xa[t], wa[e], p[t][e]);
+          for (int t = 0; t < TW; ++t)
+            if (t0 + t < T) xb[(int64_t)(t0 + t) * H + l + (j0 + jj) * kWave] = f32_to_bf16_rne(xa[jj][t]);
+        }
 #pragma unroll
-    for (int t = 0; t < TW; ++t) xa[t] = xn[t];
+        for (int t = 0; t < TW; ++t)
 #pragma unroll
-    for (int e = 0; e < EW; ++e) wa[e] = wn[e];
+          for (int e = 0; e < EW; ++e) p[t][e] = __builtin_fmaf(xa[jj][t], wa[jj][e], p[t][e]);
+      }
+    }
   }
 #pragma unroll
   for (int t = 0; t < TW; ++t)
