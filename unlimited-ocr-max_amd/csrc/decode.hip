@@ -453,7 +453,8 @@ struct Ctx {
 // before the x rows are staged, then every token's logit in the 64-lane tree
 // order, stored into each copy of the logits.
 constexpr int kMaxJ = 32;  // H <= 2048
-constexpr int kRouterWaves = 4;  // router tasks per workgroup (E = 64: the first 16 workgroups)
+constexpr int kRouterWaves = 4;   // router tasks per workgroup
+constexpr int kRouterTokens = 2;  // tokens per router task
 
 __device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A, int e, float (&w)[kMaxJ]) {
   const int l = lane();
@@ -463,11 +464,12 @@ __device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A
   for (int j = 0; j < kMaxJ; ++j) w[j] = ldg(wr + (j < nk ? j : nk - 1) * kWave);
 }
 
-__device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A, const Ctx& C, int e,
+// Logits of expert e for tokens t0 .. t1-1.
+__device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A, const Ctx& C, int e, int t0, int t1,
                                                            const float (&w)[kMaxJ]) {
   const int l = lane();
   const int nk = A.H / kWave;
-  for (int t = 0; t < A.B; ++t) {
+  for (int t = t0; t < t1; ++t) {
     const float* xr = C.xs + t * A.gh * kXPad + l;
     float p = 0.0f;
 #pragma unroll
@@ -476,7 +478,7 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
     const float v = tree_sum(p);
     if (l < kLogitCopies) st_pair(A.logits + l * kLogitCopyWords + t * 64 + e, v, C.tag);
   }
-  UOCR_TRACE(A, C.t, 4);
+  if (t0 == 0) UOCR_TRACE(A, C.t, 4);
 }
 
 // Shared gate or up, 64 columns x chunk g of H, every token: partials.
@@ -767,18 +769,22 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   C.tag = epoch + 1u;
   const int nwaves = (int)gridDim.x * kWaves;
   const int rank = wave * (int)gridDim.x + (int)blockIdx.x;
-  // Router task e runs on wave e % 4 of workgroup e / 4: workgroups that
-  // start early (the grid's start is spread over about a microsecond, and
-  // every routing waits for the last logit), few enough router rows per CU
-  // that their loads do not queue behind each other.  Every wave then takes
-  // the rest of the task list from E + rank on.
+  // Router task i (expert i % E, tokens 2(i / E) and 2(i / E) + 1) runs on
+  // wave i % 4 of workgroup i / 4: workgroups that start early (the grid's
+  // start is spread over about a microsecond, and every routing waits for
+  // the last logit), few enough router rows per CU that their loads do not
+  // queue behind each other.  Every wave then takes the rest of the task
+  // list from E + rank on.
   const int re = (int)blockIdx.x * kRouterWaves + wave;
-  const bool router = wave < kRouterWaves && re < A.E;
+  const int n_router = A.E * ((A.B + kRouterTokens - 1) / kRouterTokens);
+  const bool router = wave < kRouterWaves && re < n_router;
+  const int r_e = re % A.E;
+  const int r_t0 = (re / A.E) * kRouterTokens;
   int t = A.E + rank;
 
   // a router task's weights do not depend on x: they load while x is staged
   float w[kMaxJ];
-  if (router) router_load(A, re, w);
+  if (router) router_load(A, r_e, w);
 
   // x rows into LDS, each 128-element chunk padded to kXPad floats
   for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
@@ -791,11 +797,13 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(A.ctl + C_ARRIVED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   if (router) {
-    C.t = re;
-    UOCR_TRACE(A, re, 0);
-    router_task(A, C, re, w);
-    UOCR_TRACE(A, re, 2);
-    if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)re * 8 + 7] = rank;
+    // the trace keeps one record per expert: its first tokens' task
+    const bool traced = r_t0 == 0;
+    C.t = r_e;
+    if (traced) UOCR_TRACE(A, r_e, 0);
+    router_task(A, C, r_e, r_t0, min(A.B, r_t0 + kRouterTokens), w);
+    if (traced) UOCR_TRACE(A, r_e, 2);
+    if (traced && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
   }
   // The routing of token i is computed by wave kWaves-1-i (high waves, whose
   // tasks come late in the list); the other waves meanwhile run their tasks
@@ -878,7 +886,8 @@ hipError_t fused_grid(size_t lds_bytes, int* grid) {
 
 hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
   // every router task needs its workgroup (the routing waits for all logits)
-  if ((int64_t)grid * kRouterWaves < a.E) return hipErrorInvalidConfiguration;
+  if ((int64_t)grid * kRouterWaves < (int64_t)a.E * ((a.B + kRouterTokens - 1) / kRouterTokens))
+    return hipErrorInvalidConfiguration;
   UOCR_LAUNCH("decode_fused", k_decode_fused, dim3(grid), dim3(kThreads), lds_bytes, s, a);
   return hipGetLastError();
 }
