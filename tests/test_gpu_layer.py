@@ -243,3 +243,23 @@ def test_prefill_rows_do_not_depend_on_the_batch(oracle, full_int8) -> None:
     whole = n(moe(t(x)))
     part = n(moe(t(x[:40])))
     assert bits_equal(whole[:40], part)
+
+
+def test_unaligned_output_pointer(oracle, small) -> None:
+    """The C entry points accept an out pointer that is only 4-byte aligned (the combine's one-column path):
+    same bits as an aligned buffer, for the prefill and the multi-kernel decode (B = 40)."""
+    import ctypes
+
+    from uocr_moe import _lib
+    from uocr_moe.ops import _stream
+
+    layer = small[True]
+    moe = moe_for(layer)
+    T, H = 40, 256
+    x = t(oracle.rmsnorm_rows(np.random.default_rng(77), T, H))
+    for entry, prefill, ref in (("uocr_moe_forward", True, moe(x)), ("uocr_moe_decode_rows", False, moe.decode_rows(x))):
+        buf = torch.zeros(T * H + 1, dtype=torch.float32, device=x.device)
+        ws = moe.workspace(T, prefill)
+        _lib.call(entry, buf.data_ptr() + 4, x.data_ptr(), T, H, ctypes.byref(moe._layer), None, None, ws.data_ptr(),
+                  ws.numel(), _stream(x))
+        assert bits_equal(n(buf[1:].view(T, H)), n(ref)), entry
