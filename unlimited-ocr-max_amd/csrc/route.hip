@@ -91,17 +91,15 @@ __global__ void __launch_bounds__(256) k_logits_wide(float* __restrict__ logits,
 // k = lane + 64 j as k_logits_wide, the operands of step j + 1 loaded while
 // step j is computed, then the same 64-lane tree; the waves of the first
 // expert block also write the tokens' x rows rounded to bf16 (xb).
+// One wave's TW tokens x EW experts from token t0 and expert e0 (wave-uniform;
+// nothing to do past the ends).  xb rows are written when write_xb.
 template <int TW, int EW>
-__global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits, uint16_t* __restrict__ xb,
-                                                     const float* __restrict__ x, int64_t ldx,
-                                                     const float* __restrict__ router, int T, int E, int H,
-                                                     int32_t* __restrict__ zero, int nzero) {
-  zero_words_once(zero, nzero);
-  const int w = (int)(threadIdx.x >> 6);
+__device__ __forceinline__ void logits_tile(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                            const float* __restrict__ x, int64_t ldx,
+                                            const float* __restrict__ router, int T, int E, int H, int t0, int e0,
+                                            bool write_xb) {
+  if (t0 >= T || e0 >= E) return;
   const int l = lane_id();
-  const int e0 = (int)blockIdx.x * EW;
-  const int t0 = ((int)blockIdx.y * 4 + w) * TW;
-  if (t0 >= T || e0 >= E) return;  // wave-uniform; the kernel has no barriers
   const int nj = H / kWave;
   const float* xl = x + (int64_t)t0 * ldx + l;
   const float* wl = router + (int64_t)e0 * H + l;
@@ -110,7 +108,6 @@ __global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits,
   for (int t = 0; t < TW; ++t) xo[t] = (int64_t)min(t, T - 1 - t0) * ldx;
 #pragma unroll
   for (int e = 0; e < EW; ++e) wo[e] = (int64_t)min(e, E - 1 - e0) * H;
-  const bool write_xb = xb != nullptr && blockIdx.x == 0;
 
   float p[TW][EW];
 #pragma unroll
@@ -152,6 +149,17 @@ __global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits,
       const float v = tree_sum(p[t][e]);
       if (l == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = v;
     }
+}
+
+template <int TW, int EW>
+__global__ void __launch_bounds__(256) k_logits_tile(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                                     const float* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ router, int T, int E, int H,
+                                                     int32_t* __restrict__ zero, int nzero) {
+  zero_words_once(zero, nzero);
+  const int w = (int)(threadIdx.x >> 6);
+  logits_tile<TW, EW>(logits, xb, x, ldx, router, T, E, H, ((int)blockIdx.y * 4 + w) * TW, (int)blockIdx.x * EW,
+                      xb != nullptr && blockIdx.x == 0);
 }
 
 template <int TT, int EE>
@@ -488,6 +496,101 @@ __global__ void __launch_bounds__(kScatterThreads) k_group_scatter(const int32_t
   }
 }
 
+// ---------------------------------------------------------------- prefill routing, T below 2048
+//
+// k_logits_topk: a workgroup of 8 waves owns 4 tokens and every expert
+// (E <= 64): wave w computes the 4 tokens' logits of experts 8w .. 8w+7 (the
+// tile kernel's chains and trees: the same bits), then, after a barrier,
+// waves 0-3 run one token's softmax + top-k each, and the workgroup's rows per expert go to hist[b] (every expert,
+// zeros included).  k_group_scatter_hist: workgroup b sums hist over all
+// counting workgroups and over those before it, derives the tables
+// (workgroup 0 writes them) and places its rows.  No counters to clear.
+
+constexpr int kFusedTokens = 4;
+
+__global__ void __launch_bounds__(512) k_logits_topk(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                                     const float* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ router, int T, int E, int H, int topk,
+                                                     int renorm, int32_t* __restrict__ ids32, float* __restrict__ wts,
+                                                     int32_t* __restrict__ hist) {
+  __shared__ int cnt[64];
+  __shared__ int ids_lds[kFusedTokens * 64];
+  const int b = (int)blockIdx.x;
+  const int w = (int)(threadIdx.x >> 6);
+  const int tid = (int)threadIdx.x;
+  const int t0 = b * kFusedTokens;
+  if (tid < 64) cnt[tid] = 0;
+  logits_tile<kFusedTokens, 8>(logits, xb, x, ldx, router, T, E, H, t0, 8 * w, xb != nullptr && w == 0);
+  __syncthreads();  // the workgroup's logits (global) are visible to all its waves
+  const int t = t0 + w;
+  if (w < kFusedTokens && t < T) {
+    const int64_t o = (int64_t)t * topk;
+    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + w * topk);
+  }
+  __syncthreads();
+  const int rows = (min(T, t0 + kFusedTokens) - t0) * topk;
+  for (int r = tid; r < rows; r += 512) atomicAdd(&cnt[clamp_expert(ids_lds[r], E)], 1);
+  __syncthreads();
+  if (tid < E) stg(hist + (int64_t)b * E + tid, cnt[tid]);
+}
+
+__global__ void __launch_bounds__(256) k_group_scatter_hist(const int32_t* __restrict__ ids, int T, int E, int topk,
+                                                            int bm, int blocks, const int32_t* __restrict__ hist,
+                                                            GroupTables g) {
+  __shared__ int part_before[4][64];
+  __shared__ int part_tot[4][64];
+  __shared__ int cursor[64];
+  const int b = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  const int e = tid & 63;
+  const int c = tid >> 6;
+  // four threads per expert, each over every fourth counting workgroup
+  int before = 0, tot = 0;
+  if (e < E) {
+#pragma unroll 4
+    for (int v = c; v < blocks; v += 4) {
+      const int h = ldg(hist + (int64_t)v * E + e);
+      before += v < b ? h : 0;
+      tot += h;
+    }
+  }
+  part_before[c][e] = before;
+  part_tot[c][e] = tot;
+  __syncthreads();
+  if (tid < 64) {
+    // per-expert sums (in a fixed order), then the scans over the experts in one wave
+    before = part_before[0][e] + part_before[1][e] + part_before[2][e] + part_before[3][e];
+    tot = e < E ? part_tot[0][e] + part_tot[1][e] + part_tot[2][e] + part_tot[3][e] : 0;
+    const int tiles = tot > 0 ? (tot + bm - 1) / bm : 0;
+    const int nz = tot > 0 ? 1 : 0;
+    const int ic = wave_inclusive_sum(tot), it = wave_inclusive_sum(tiles), in = wave_inclusive_sum(nz);
+    const int start = ic - tot, tile0 = it - tiles, grp = in - nz;
+    if (e < E) {
+      cursor[e] = start + before;
+      if (b == 0) {
+        if (tot > 0) {
+          stg(g.group_expert + grp, e);
+          stg(g.group_start + grp, start);
+          if (g.tile_start) stg(g.tile_start + grp, tile0);
+        }
+        if (e == E - 1) {
+          stg(g.group_start + grp + nz, start + tot);
+          if (g.tile_start) stg(g.tile_start + grp + nz, tile0 + tiles);
+          stg(g.n_groups, grp + nz);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t r0 = (int64_t)b * kFusedTokens * topk;
+  const int64_t r1 = min((int64_t)T * topk, r0 + (int64_t)kFusedTokens * topk);
+  for (int64_t r = r0 + tid; r < r1; r += 256) {
+    const int pos = atomicAdd(&cursor[clamp_expert(ldg(ids + r), E)], 1);
+    stg(g.group_rows + pos, (int32_t)r);
+    if (g.inv) stg(g.inv + r, pos);
+  }
+}
+
 constexpr int kSmallTokens = 64;
 
 __global__ void __launch_bounds__(1024) k_route_small(const float* __restrict__ logits, int T, int E, int topk,
@@ -612,6 +715,21 @@ hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int re
               wts, total, base);
   UOCR_LAUNCH("group_scatter", k_group_scatter, dim3((blocks + kScatterSpan - 1) / kScatterSpan),
               dim3(kScatterThreads), 0, s, ids32, T, E, topk, bm, total, base, g);
+  return hipGetLastError();
+}
+
+int fused_route_blocks(int T) { return (T + kFusedTokens - 1) / kFusedTokens; }
+
+hipError_t launch_logits_topk_group(float* logits, uint16_t* xb, const float* x, int64_t ldx, const float* router,
+                                    int T, int E, int H, int topk, int renorm, int32_t* ids32, float* wts, int bm,
+                                    const GroupTables& g, int32_t* hist, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (E > 64 || H % kWave != 0 || topk > 64) return hipErrorInvalidValue;
+  const int blocks = fused_route_blocks(T);
+  UOCR_LAUNCH("logits_topk", k_logits_topk, dim3(blocks), dim3(512), 0, s, logits, xb, x, ldx, router, T, E, H, topk,
+              renorm, ids32, wts, hist);
+  UOCR_LAUNCH("group_scatter", k_group_scatter_hist, dim3(blocks), dim3(256), 0, s, ids32, T, E, topk, bm, blocks,
+              hist, g);
   return hipGetLastError();
 }
 

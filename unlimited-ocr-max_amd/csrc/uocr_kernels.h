@@ -104,6 +104,13 @@ constexpr int kRouteMaxExperts = 256;
 int route_count_blocks(int T);
 hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
                              int bm, const GroupTables& g, int32_t* total, int32_t* base, hipStream_t s);
+// Prefill routing for T < 2048 (E <= 64): logits, softmax + top-k and
+// per-workgroup counts in one launch (xb as launch_logits), then the
+// grouping.  hist holds fused_route_blocks(T) * E ints of scratch.
+int fused_route_blocks(int T);
+hipError_t launch_logits_topk_group(float* logits, uint16_t* xb, const float* x, int64_t ldx, const float* router,
+                                    int T, int E, int H, int topk, int renorm, int32_t* ids32, float* wts, int bm,
+                                    const GroupTables& g, int32_t* hist, hipStream_t s);
 // Decode-size routing in one workgroup: softmax + top-k of T <= 64 tokens, then
 // the grouping of their T*topk rows.
 hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,

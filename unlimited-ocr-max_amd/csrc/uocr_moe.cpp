@@ -505,6 +505,7 @@ struct PrefillBufs {
   float* sh;
   int32_t* total;  // rows per expert (routing counters)
   int32_t* base;   // per counting workgroup: its first place per expert
+  int32_t* hist;   // per counting workgroup: its rows per expert (T < 2048)
 };
 
 static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
@@ -521,6 +522,7 @@ static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
   d.sh = c.take<float>(T * L->hidden);
   d.total = c.take<int32_t>(L->num_experts);
   d.base = c.take<int32_t>((int64_t)route_count_blocks((int)T) * L->num_experts);
+  d.hist = c.take<int32_t>((int64_t)fused_route_blocks((int)T) * L->num_experts);
   return d;
 }
 
@@ -722,14 +724,18 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   const PrefillBufs d = carve_prefill(c, L, T);
   const int E = (int)L->num_experts, H = (int)L->hidden, F = (int)L->ffn, Fs = (int)L->shared_ffn;
 
-  const bool many = E <= kRouteMaxExperts;
-  hipError_t e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s, many ? d.total : nullptr, E);
-  if (e == hipSuccess && many) {
-    e = launch_topk_group(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, d.wts, BM, d.g, d.total, d.base,
-                          s);
-  } else if (e == hipSuccess) {
-    e = launch_softmax_topk(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, nullptr, d.wts, s);
-    if (e == hipSuccess) e = launch_group(d.ids, (int)R, E, BM, d.g, s);
+  // routing (E <= 64 here): below 2048 tokens one launch computes the logits, the top-k and
+  // per-workgroup counts; above, the logits tiles share router rows over more tokens and the
+  // top-k runs in its own launch
+  hipError_t e = hipSuccess;
+  if (T < 2048) {
+    e = launch_logits_topk_group(d.logits, d.xb, x, H, L->router, (int)T, E, H, (int)L->top_k, L->renormalize, d.ids,
+                                 d.wts, BM, d.g, d.hist, s);
+  } else {
+    e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s, d.total, E);
+    if (e == hipSuccess)
+      e = launch_topk_group(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, d.wts, BM, d.g, d.total, d.base,
+                            s);
   }
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
   const int max_groups = (int)(E < R ? E : R);
