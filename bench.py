@@ -216,6 +216,27 @@ def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: st
     return res
 
 
+def bench_dense(N: int, K: int, device: str, rows=(1, 8), copies: int = 2, launches: int = 40) -> dict:
+    """dense_bf16_qmv at one projection's shape (lm_head: 129280 x 1280): `copies` K-blocked bf16
+    weights (2 x 331 MB > the 256 MB MALL, so each launch reads its weight cold), graph-timed."""
+    import torch
+    import uocr_moe
+
+    g = torch.Generator(device=device).manual_seed(N + K)
+    ws = [(torch.randn((K // 16, N, 16), generator=g, device=device) * 0.05).to(torch.bfloat16) for _ in range(copies)]
+    out = {}
+    for m in rows:
+        xs = [torch.randn((m, K), generator=g, device=device) for _ in range(copies)]
+        fns = [lambda i=i: uocr_moe.ops.dense_bf16_qmv(xs[i % copies], ws[i % copies]) for i in range(launches)]
+        us = time_graph(graph_of(fns)) * 1e3 / launches
+        nbytes = N * K * 2 + m * K * 4 + m * N * 4
+        out[f"m{m}"] = {"us": round(us, 3), "bytes": nbytes, "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del ws
+    torch.cuda.empty_cache()
+    return out
+
+
 def zipf_prefill_inputs(g, T: int, device: str, seed: int):
     """274 vision + 238 text rows of N(0,1) (per 512); a constant feature carries a Zipf(1.1) expert bias."""
     import torch
@@ -454,6 +475,9 @@ def main() -> int:
     if not args.quick:
         del layers_w, layers
         torch.cuda.empty_cache()
+        log("dense_bf16_qmv at lm_head's shape (129280 x 1280), M=1/8")
+        results["dense_bf16_lm_head"] = bench_dense(129280, H, dev)
+        log(f"  {results['dense_bf16_lm_head']}")
         log("decode bf16 B=1/8")
         bf = [make_layer(2000 + l, False, dev)[0] for l in range(LAYERS)]
         results["decode_bf16_b1"] = bench_decode(bf, 1, args.steps, args.warmup, False, dev, 101)

@@ -284,10 +284,11 @@ def test_dense_column_slice_activation(ops, oracle) -> None:
     assert bits_equal(got, n(ops.dense_bf16_qmv(t(np.ascontiguousarray(xw[:, 1:65])), t(w), tile=4)))
 
 
-@pytest.mark.parametrize(("n_", "k"), [(1280, 1280), (6848, 1280), (1280, 6848), (1792, 1280), (1280, 1792)],
-                         ids=["attention", "dense_gate_up", "dense_down", "shared_gate_up", "shared_down"])
+@pytest.mark.parametrize(("n_", "k"), [(1280, 1280), (6848, 1280), (1280, 6848), (1792, 1280), (1280, 1792),
+                                        (129280, 1280)],
+                         ids=["attention", "dense_gate_up", "dense_down", "shared_gate_up", "shared_down", "lm_head"])
 def test_dense_real_shapes(ops, oracle, n_, k) -> None:
-    """tests/test_kernels_dense_bf16.py:203-223 at M = 1 and 8."""
+    """tests/test_kernels_dense_bf16.py:203-223 at M = 1 and 8; lm_head's width is tests/test_dense_tile.py:20."""
     for m in (1, 8):
         rng = np.random.default_rng(n_ + k + m)
         x = rng.standard_normal((m, k)).astype(np.float32)
