@@ -6,6 +6,7 @@ reference's op names (:mod:`uocr_moe.ops`) and MoE module (:mod:`uocr_moe.moe`).
 """
 
 from ._lib import LIB_PATH, UocrError
+from .checkpoint import WeightMappingError, load_safetensors, moe_from_checkpoint, moe_layer_weights
 from .moe import MoE, MoeConfig, gate
 from .ops import (
     custom,
@@ -22,12 +23,16 @@ __all__ = [
     "MoE",
     "MoeConfig",
     "UocrError",
+    "WeightMappingError",
     "custom",
     "dense_bf16_qmv",
     "gate",
     "int8_dequant_expert",
     "kblocked",
+    "load_safetensors",
     "moe_bf16_qmv",
+    "moe_from_checkpoint",
     "moe_int8_qmv",
+    "moe_layer_weights",
     "quantize_per_group",
 ]
