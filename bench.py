@@ -237,6 +237,31 @@ def bench_dense(N: int, K: int, device: str, rows=(1, 8), copies: int = 2, launc
     return out
 
 
+def bench_ngram(device: str, rows: int = 8, vocab: int = 129280, window: int = 128, ngram: int = 35,
+                copies: int = 64, launches: int = 64) -> dict:
+    """ngram_block over `rows` x `vocab` logits (the decode step's guard, n = 35 over the 128-id window);
+    `copies` logits buffers (265 MB, beyond the MALL) so each launch reads cold, graph-timed."""
+    import torch
+    import uocr_moe
+
+    g = torch.Generator(device=device).manual_seed(35)
+    logits = [torch.randn((rows, vocab), generator=g, device=device) for _ in range(copies)]
+    outs = [torch.empty_like(x) for x in logits[:2]]
+    motif = torch.randint(0, vocab, (rows, 40), generator=g, device=device, dtype=torch.int32)
+    fill = torch.randint(0, vocab, (rows, window - 80), generator=g, device=device, dtype=torch.int32)
+    history = torch.cat([motif, fill, motif], dim=1).contiguous()  # the last 34 ids recur: bans happen
+    n = torch.tensor([ngram], dtype=torch.int32, device=device)
+    fns = [lambda i=i: uocr_moe.ops.ngram_block(logits[i % copies], history, n, out=outs[i % 2])
+           for i in range(launches)]
+    us = time_graph(graph_of(fns)) * 1e3 / launches
+    nbytes = 2 * rows * vocab * 4 + rows * window * 4
+    del logits, outs
+    torch.cuda.empty_cache()
+    return {"rows": rows, "vocab": vocab, "window": window, "ngram": ngram, "us": round(us, 3), "bytes": nbytes,
+            "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def zipf_prefill_inputs(g, T: int, device: str, seed: int):
     """274 vision + 238 text rows of N(0,1) (per 512); a constant feature carries a Zipf(1.1) expert bias."""
     import torch
@@ -475,6 +500,9 @@ def main() -> int:
     if not args.quick:
         del layers_w, layers
         torch.cuda.empty_cache()
+        log("ngram_block, 8 x 129280 logits, n = 35 over 128 ids")
+        results["ngram_block_b8"] = bench_ngram(dev)
+        log(f"  {results['ngram_block_b8']}")
         log("dense_bf16_qmv at lm_head's shape (129280 x 1280), M=1/8")
         results["dense_bf16_lm_head"] = bench_dense(129280, H, dev)
         log(f"  {results['dense_bf16_lm_head']}")

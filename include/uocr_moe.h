@@ -75,6 +75,20 @@ int uocr_int8_dequant_expert(void* result, int64_t result_n, int64_t result_kdim
                              const int32_t* expert_idx, int64_t idx_len,
                              void* stream, char* err, size_t errlen);
 
+/* ngram_block -- replaces NgramBlock.execute
+ * (unlimited_ocr_max/kernels/ngram_block.mojo:60-151; staged by apply_ngram_guard,
+ * unlimited_ocr_max/ngram.py:33-53).
+ *   result fp32 [rows, vocab], logits fp32 [rows, vocab], history int32 [rows, hist_len]
+ *   (each row's last `window` ids, newest last), ngram int32 [1] (device).  A rank-1
+ *   call is rows = 1.  Row b's id v is set to -3.0e38 when some n-gram of history
+ *   row b ends in v and its first n-1 ids equal the row's last n-1 ids (n == 1: every
+ *   id of the history); n < 1 or hist_len < n leaves the row unchanged.  result may
+ *   be logits (in place).  hist_len <= 8192. */
+int uocr_ngram_block(float* result, int64_t result_rows, int64_t result_vocab, const float* logits,
+                     int64_t logits_rows, int64_t logits_vocab, const int32_t* history, int64_t hist_rows,
+                     int64_t hist_len, const int32_t* ngram, int64_t ngram_len, void* stream, char* err,
+                     size_t errlen);
+
 /* dense_bf16_qmv -- replaces DenseBf16Qmv.execute[tile]
  * (unlimited_ocr_max/kernels/dense_bf16.mojo:119-158; staged by
  * dense_bf16_qmv, unlimited_ocr_max/decoder.py:166-184).

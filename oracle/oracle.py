@@ -434,6 +434,63 @@ def moe_layer_f64(x, layer: MoeWeights, ids=None, wts=None, bf16_dequant: bool =
 
 
 # ---------------------------------------------------------------------------
+# the n-gram guard (unlimited_ocr_max/kernels/ngram_block.mojo)
+# ---------------------------------------------------------------------------
+
+#: ngram_block.mojo:49, as the float32 it lands in.
+NGRAM_BLOCKED = np.float32(-3.0e38)
+
+
+def ngram_banned(sequence, ngram_size: int, window: int) -> set[int]:
+    """The reference processor's banned ids, over the WHOLE sequence with an explicit window
+    (``SlidingWindowNoRepeatNgramProcessor`` as restated in ngram_block.mojo:5-15)."""
+    ids = [int(i) for i in sequence]
+    if ngram_size < 1 or len(ids) < ngram_size:
+        return set()
+    search_start = max(0, len(ids) - window)
+    search_end = len(ids) - ngram_size + 1
+    prefix = tuple(ids[len(ids) - (ngram_size - 1):]) if ngram_size > 1 else ()  # sequence[-0:] is all of it
+    banned: set[int] = set()
+    for idx in range(search_start, search_end):
+        gram = ids[idx: idx + ngram_size]
+        if ngram_size == 1 or tuple(gram[:-1]) == prefix:
+            banned.add(gram[-1])
+    return banned
+
+
+def ngram_banned_per_id(history, ngram_size: int, vocab: int) -> set[int]:
+    """The same set as the op's work items compute it (ngram_block.mojo:112-146): for every vocabulary id,
+    a scan of every start of the windowed history.  Brute force, for small vocabularies."""
+    h = [int(i) for i in history]
+    if ngram_size < 1 or len(h) < ngram_size:
+        return set()
+    prefix_len = ngram_size - 1
+    starts = len(h) - ngram_size + 1
+    prefix_at = len(h) - prefix_len
+    out = set()
+    for token in range(vocab):
+        for start in range(starts):
+            if h[start + prefix_len] != token:
+                continue
+            if all(h[start + j] == h[prefix_at + j] for j in range(prefix_len)):
+                out.add(token)
+                break
+    return out
+
+
+def ngram_block(logits: np.ndarray, history: np.ndarray, ngram_size: int) -> np.ndarray:
+    """The op: ``logits [V]`` / ``[B, V]`` with row b's banned ids (from history row b, the row's last
+    ids) set to :data:`NGRAM_BLOCKED`; ids outside ``[0, V)`` ban nothing."""
+    out = np.array(logits, dtype=np.float32, copy=True)
+    rows = out.reshape(-1, out.shape[-1])
+    hist = np.asarray(history).reshape(rows.shape[0], -1)
+    for b in range(rows.shape[0]):
+        banned = [v for v in ngram_banned(hist[b], ngram_size, hist.shape[1]) if 0 <= v < rows.shape[1]]
+        rows[b, banned] = NGRAM_BLOCKED
+    return out
+
+
+# ---------------------------------------------------------------------------
 # synthetic layers
 # ---------------------------------------------------------------------------
 

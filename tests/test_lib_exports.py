@@ -27,7 +27,7 @@ def _declared() -> list[str]:
 def test_header_declares_the_entry_points() -> None:
     names = _declared()
     for want in ("uocr_moe_int8_qmv", "uocr_moe_bf16_qmv", "uocr_int8_dequant_expert", "uocr_dense_bf16_qmv",
-                 "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward"):
+                 "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward", "uocr_ngram_block"):
         assert want in names
 
 
@@ -90,6 +90,20 @@ def test_dense_refusals() -> None:
         "dense_bf16_qmv: w is not K-blocked by KBLOCK"
     assert _err("uocr_dense_bf16_qmv", None, 2, 4, None, 2, 32, None, 2, 4, 16, 0, None) == \
         "dense_bf16_qmv: tile must be >= 1"
+
+
+def test_ngram_refusals() -> None:
+    """unlimited_ocr_max/kernels/ngram_block.mojo:85-99."""
+    # (result rows, vocab, logits rows, vocab, history rows, length, ngram count)
+    cases = [
+        ((2, 16, 2, 15, 2, 4, 1), "ngram_block: logits and output disagree on shape"),
+        ((2, 16, 2, 16, 1, 4, 1), "ngram_block: history and logits disagree on the row count"),
+        ((2, 16, 2, 16, 2, 4, 2), "ngram_block: `ngram` must be a single int32"),
+        ((2, 16, 2, 16, 2, 0, 1), "ngram_block: history is empty"),
+        ((2, 16, 2, 16, 2, 8193, 1), "ngram_block: history longer than 8192 ids"),
+    ]
+    for (rr, rv, lr, lv, hr, hl, nl), message in cases:
+        assert _err("uocr_ngram_block", None, rr, rv, None, lr, lv, None, hr, hl, None, nl, None) == message
 
 
 def test_layer_refusals() -> None:

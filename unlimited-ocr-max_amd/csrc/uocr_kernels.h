@@ -154,6 +154,14 @@ struct GemmProblem {
 hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
                             hipStream_t s);
 
+// ---- the n-gram logit guard (ngram.hip) ----
+
+constexpr int kNgramMaxHistory = 8192;
+// result [rows, vocab] = logits with every banned id set to BLOCKED; history
+// [rows, hist_len] int32, ngram int32 [1] (device).  result may alias logits.
+hipError_t launch_ngram_block(float* result, const float* logits, int64_t rows, int64_t vocab,
+                              const int32_t* history, int hist_len, const int32_t* ngram, hipStream_t s);
+
 // ---- the persistent decode layer (decode.hip) ----
 
 constexpr int kFusedWaves = 12;  // waves per workgroup, one workgroup per CU (168 VGPRs a lane)

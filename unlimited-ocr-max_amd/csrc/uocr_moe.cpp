@@ -383,6 +383,27 @@ int uocr_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n, const
   return e == hipSuccess ? 0 : hip_fail(err, errlen, "dense_bf16_qmv", e);
 }
 
+// ------------------------------------------------------------------ the n-gram guard
+
+int uocr_ngram_block(float* result, int64_t result_rows, int64_t result_vocab, const float* logits,
+                     int64_t logits_rows, int64_t logits_vocab, const int32_t* history, int64_t hist_rows,
+                     int64_t hist_len, const int32_t* ngram, int64_t ngram_len, void* stream, char* err,
+                     size_t errlen) {
+  // unlimited_ocr_max/kernels/ngram_block.mojo:85-99
+  if (logits_rows != result_rows || logits_vocab != result_vocab)
+    return fail(err, errlen, "ngram_block: logits and output disagree on shape");
+  if (hist_rows != result_rows) return fail(err, errlen, "ngram_block: history and logits disagree on the row count");
+  if (ngram_len != 1) return fail(err, errlen, "ngram_block: `ngram` must be a single int32");
+  if (hist_len < 1) return fail(err, errlen, "ngram_block: history is empty");
+  if (hist_len > kNgramMaxHistory)
+    return fail(err, errlen, "ngram_block: history longer than %d ids", kNgramMaxHistory);
+  if (result_rows < 0 || result_vocab < 0 || result_rows > 65535)
+    return fail(err, errlen, "ngram_block: bad logits shape");
+  const hipError_t e = launch_ngram_block(result, logits, result_rows, result_vocab, history, (int)hist_len, ngram,
+                                          (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, "ngram_block", e);
+}
+
 // ------------------------------------------------------------------ the MoE block
 
 static int check_layer(const char* op, const uocr_moe_layer* L, int64_t hidden, char* err, size_t errlen) {

@@ -15,6 +15,7 @@ from .ops import (
     kblocked,
     moe_bf16_qmv,
     moe_int8_qmv,
+    ngram_block,
     quantize_per_group,
 )
 
@@ -34,5 +35,6 @@ __all__ = [
     "moe_from_checkpoint",
     "moe_int8_qmv",
     "moe_layer_weights",
+    "ngram_block",
     "quantize_per_group",
 ]

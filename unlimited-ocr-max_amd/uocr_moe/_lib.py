@@ -48,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "uocr_int8_dequant_expert": [_vp, _i64, _i64, _int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64,
                                  _vp, _cp, _sz],
     "uocr_dense_bf16_qmv": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _cp, _sz],
+    "uocr_ngram_block": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _cp, _sz],
     "uocr_moe_workspace_bytes": [ctypes.POINTER(Layer), _i64, _int],
     "uocr_moe_gate": [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _int, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_decode_rows": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],

@@ -140,11 +140,43 @@ def dense_bf16_qmv(x, w, *, tile: int | None = None, out: torch.Tensor | None = 
     return out
 
 
+#: The value a banned logit is set to (unlimited_ocr_max/kernels/ngram_block.mojo:49): finite, below every logit.
+NGRAM_BLOCKED = -3.0e38
+
+
+def ngram_block(logits, history, ngram, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The no-repeat-n-gram guard (unlimited_ocr_max/kernels/ngram_block.mojo:1-151).
+
+    ``logits [V]`` with ``history [H]`` (one row), or ``logits [B, V]`` with ``history [B, H]``: row ``b``
+    against row ``b``'s last ids only.  ``ngram`` is an int32 ``[1]`` tensor on the GPU (read on the device,
+    as the reference's) or a Python int.  Banned ids become :data:`NGRAM_BLOCKED`; ``out`` may be ``logits``.
+    """
+    op = "ngram_block"
+    if not isinstance(logits, torch.Tensor) or logits.dim() not in (1, 2):
+        raise ValueError(f"{op} takes one row (V,) or B rows (B, V)")
+    rank = logits.dim()
+    logits = _gpu(op, "logits", logits, torch.float32, rank)
+    history = _gpu(op, "history", history, torch.int32, rank)
+    if isinstance(ngram, int):
+        ngram = torch.tensor([ngram], dtype=torch.int32, device=logits.device)
+    ngram = _gpu(op, "ngram", ngram, torch.int32, 1)
+    if out is None:
+        out = torch.empty_like(logits)
+    out = _gpu(op, "result", out, torch.float32, rank)
+    rows = 1 if rank == 1 else int(logits.shape[0])
+    hrows = 1 if rank == 1 else int(history.shape[0])
+    orows = 1 if rank == 1 else int(out.shape[0])
+    _lib.call("uocr_ngram_block", out.data_ptr(), orows, out.shape[-1], logits.data_ptr(), rows, logits.shape[-1],
+              history.data_ptr(), hrows, history.shape[-1], ngram.data_ptr(), ngram.shape[0], _stream(logits))
+    return out
+
+
 _OPS = {
     "moe_int8_qmv": moe_int8_qmv,
     "moe_bf16_qmv": moe_bf16_qmv,
     "int8_dequant_expert": int8_dequant_expert,
     "dense_bf16_qmv": dense_bf16_qmv,
+    "ngram_block": ngram_block,
 }
 
 
