@@ -96,11 +96,11 @@ struct GroupTables {
 };
 // Groups R rows by their clamped expert id (ascending expert).
 hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s);
-// Prefill routing over many workgroups (E <= 256): softmax + top-k of T
+// Prefill routing over many workgroups (E <= 64): softmax + top-k of T
 // tokens, then the grouping of their T*topk rows.  `total` (E ints) must be
 // zero when the first kernel starts (launch_logits clears it); `base` holds
 // route_count_blocks(T) * E ints of scratch.
-constexpr int kRouteMaxExperts = 256;
+constexpr int kRouteMaxExperts = 64;  // a lane per expert in the top-k
 int route_count_blocks(int T);
 hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
                              int bm, const GroupTables& g, int32_t* total, int32_t* base, hipStream_t s);
