@@ -262,6 +262,51 @@ def bench_ngram(device: str, rows: int = 8, vocab: int = 129280, window: int = 1
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_attention(device: str, rows: int, attend: int = 640, layers: int = 12, heads: int = 10, head_dim: int = 128,
+                    page_size: int = 128, sweeps: int = 4) -> dict:
+    """paged_decode_attention at the served pool: 8 requests x 5 pages (512 prompt rows + the 128-row ring)
+    plus the null page, 12 layers of 10 x 128 fp32 heads (645 MB, beyond the MALL).  `rows` requests attend
+    `attend` rows each and append at row attend - 1; a graph walks the layers `sweeps` times, so every call
+    reads its layer's rows cold."""
+    import math
+
+    import torch
+    import uocr_moe
+
+    per = math.ceil(attend / page_size)
+    pages = 8 * per + 1
+    g = torch.Generator(device=device).manual_seed(640)
+    pool = torch.randn((pages, 2, layers, page_size, heads, head_dim), generator=g, device=device)
+    order = torch.randperm(pages - 1, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    lut = torch.full((rows, per + 1), pages - 1, dtype=torch.int32)
+    lut[:, :per] = order[: rows * per].reshape(rows, per)
+    kv = uocr_moe.PagedKv(kv_blocks=pool, lookup_table=lut.to(device),
+                          attend_lengths=torch.full((rows,), attend - 1, dtype=torch.int32, device=device),
+                          attend_max=attend, write_index=torch.full((rows,), attend - 1, dtype=torch.int32,
+                                                                    device=device))
+    q, k_new, v_new = (torch.randn((rows, heads, head_dim), generator=g, device=device) for _ in range(3))
+    out = torch.empty_like(q)
+    from uocr_moe import _lib
+
+    ws = torch.empty(_lib.load().uocr_paged_attention_workspace_bytes(rows, heads, attend) // 4 + 4,
+                     device=device)
+    scale = 1.0 / math.sqrt(head_dim)
+    fns = [lambda l=l: uocr_moe.paged_decode_attention(q, k_new, v_new, kv=kv, layer_idx=l % layers, scale=scale,
+                                                       out=out, workspace=ws)
+           for l in range(layers * sweeps)]
+    us = time_graph(graph_of(fns)) * 1e3 / len(fns)
+    kt = kernel_times(fns[:layers])
+    part_us = 1e3 * statistics.mean(kt["attn_partial"])
+    nbytes = rows * heads * attend * head_dim * 4 * 2
+    del pool, kv
+    torch.cuda.empty_cache()
+    return {"rows": rows, "attend": attend, "heads": heads, "head_dim": head_dim, "us_per_layer": round(us, 3),
+            "partial_kernel_us": round(part_us, 3), "bytes": nbytes,
+            "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "partial_hbm_frac": round(nbytes / (part_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def zipf_prefill_inputs(g, T: int, device: str, seed: int):
     """274 vision + 238 text rows of N(0,1) (per 512); a constant feature carries a Zipf(1.1) expert bias."""
     import torch
@@ -503,6 +548,10 @@ def main() -> int:
         log("ngram_block, 8 x 129280 logits, n = 35 over 128 ids")
         results["ngram_block_b8"] = bench_ngram(dev)
         log(f"  {results['ngram_block_b8']}")
+        log("paged_decode_attention, 640 rows attended, B=1/8")
+        for B in (1, 8):
+            results[f"paged_attention_b{B}"] = bench_attention(dev, B)
+            log(f"  {results[f'paged_attention_b{B}']}")
         log("dense_bf16_qmv at lm_head's shape (129280 x 1280), M=1/8")
         results["dense_bf16_lm_head"] = bench_dense(129280, H, dev)
         log(f"  {results['dense_bf16_lm_head']}")

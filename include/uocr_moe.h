@@ -15,7 +15,8 @@
  * patterns.  The library keeps no pointer past the call.  Scratch memory for
  * the grouping tables and the layer intermediates comes from the `workspace`
  * argument when one is given (size: uocr_moe_workspace_bytes), else from a
- * buffer the library keeps per device and stream (grown on demand).
+ * buffer the library keeps per device and stream (grown on demand, so a call
+ * under stream capture passes its own workspace).
  */
 #ifndef UOCR_MOE_H
 #define UOCR_MOE_H
@@ -88,6 +89,35 @@ int uocr_ngram_block(float* result, int64_t result_rows, int64_t result_vocab, c
                      int64_t logits_rows, int64_t logits_vocab, const int32_t* history, int64_t hist_rows,
                      int64_t hist_len, const int32_t* ngram, int64_t ngram_len, void* stream, char* err,
                      size_t errlen);
+
+/* paged_decode_attention -- replaces paged_decode_attention
+ * (unlimited_ocr_max/decoder.py:425-437: store_k/v_cache_ragged at the write
+ * index, then flash_attention_ragged under the causal mask; the pool and its
+ * step metadata of unlimited_ocr_max/kv_cache.py:1-36 and :305-329).
+ *   out, q, k_new, v_new fp32 [rows, heads, head_dim] (post-RoPE), head_dim 128;
+ *   kv_blocks fp32 [pages, 2, layers, page_size, heads, head_dim], page_size a
+ *   multiple of 128; lookup uint32 [rows, lookup_cols]; attend_lengths uint32
+ *   [rows] = attend_len - 1; write_index uint32 [rows] (all device);
+ *   attend_max (host) = the largest attend_len.  Logical row r of batch row b is
+ *   slot r % page_size of page lookup[b, r / page_size].  Stores k_new / v_new
+ *   at row write_index[b] of layer `layer`, then
+ *   out[b,h] = sum_{r < attend_len} softmax_r(scale * q[b,h] . k_r) v_r,
+ *   fp32 throughout.  Device metadata past what the lookup row addresses is
+ *   clamped there (a write index past it stores nothing).  workspace may be
+ *   NULL (the library's own) or at least
+ *   uocr_paged_attention_workspace_bytes(rows, heads, attend_max) bytes,
+ *   16-byte aligned.  Up to 65536 (row, head) pairs merge their splits inside
+ *   the one launch, with per-device counters that the first call outside
+ *   stream capture allocates; each stream takes one of 16 slots of them, and
+ *   launches on streams that share a slot must not overlap in time. */
+size_t uocr_paged_attention_workspace_bytes(int64_t rows, int64_t heads, int64_t attend_max);
+int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, const float* v_new,
+                                int64_t rows, int64_t heads, int64_t head_dim,
+                                float* kv_blocks, int64_t pages, int64_t layers, int64_t page_size,
+                                int64_t layer, const uint32_t* lookup, int64_t lookup_cols,
+                                const uint32_t* attend_lengths, int64_t attend_max,
+                                const uint32_t* write_index, float scale, void* workspace,
+                                size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
 /* dense_bf16_qmv -- replaces DenseBf16Qmv.execute[tile]
  * (unlimited_ocr_max/kernels/dense_bf16.mojo:119-158; staged by

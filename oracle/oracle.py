@@ -491,6 +491,48 @@ def ngram_block(logits: np.ndarray, history: np.ndarray, ngram_size: int) -> np.
 
 
 # ---------------------------------------------------------------------------
+# paged decode attention (unlimited_ocr_max/decoder.py:425-437 over kv_cache.py's pool)
+# ---------------------------------------------------------------------------
+
+
+def paged_row(kv_blocks: np.ndarray, lookup_row: np.ndarray, r: int, kv: int, layer: int) -> np.ndarray:
+    """Logical row ``r`` of one request, ``[heads, D]``: slot ``r % P`` of page ``lookup_row[r // P]``
+    (kv_cache.py:17-19) in ``kv_blocks [pages, 2, layers, P, heads, D]``."""
+    P = kv_blocks.shape[3]
+    return kv_blocks[int(lookup_row[r // P]), kv, layer, r % P]
+
+
+def paged_decode_attention(q, k_new, v_new, kv_blocks, lookup, attend_lengths, write_index, layer: int,
+                           scale: float) -> tuple[np.ndarray, np.ndarray]:
+    """``(out float64 [B, heads, D], the pool after the store)``.
+
+    The store (store_k/v_cache_ragged at ``write_index``, decoder.py:434-435) on a copy of the pool, then
+    per row ``b`` the chain the reference's test holds the op to (tests/test_kv_cache.py:339-349): the
+    rows ``[0, attend_lengths[b] + 1)``, read back through the lookup table, ``softmax(q k^T * scale) @ v``
+    in float64.  Rows are stored in order, so two rows that write one slot leave the later row's values,
+    and row ``b`` reads the pool after every store.
+    """
+    pool = np.array(kv_blocks, dtype=np.float32, copy=True)
+    B = q.shape[0]
+    P = pool.shape[3]
+    for b in range(B):
+        w = int(write_index[b])
+        page = int(lookup[b, w // P])
+        pool[page, 0, layer, w % P] = k_new[b]
+        pool[page, 1, layer, w % P] = v_new[b]
+    out = np.zeros(q.shape, np.float64)
+    for b in range(B):
+        n = int(attend_lengths[b]) + 1
+        k = np.stack([paged_row(pool, lookup[b], r, 0, layer) for r in range(n)]).astype(np.float64)  # [n, h, D]
+        v = np.stack([paged_row(pool, lookup[b], r, 1, layer) for r in range(n)]).astype(np.float64)
+        scores = np.einsum("hd,lhd->hl", q[b].astype(np.float64), k) * scale
+        weights = np.exp(scores - scores.max(axis=-1, keepdims=True))
+        weights /= weights.sum(axis=-1, keepdims=True)
+        out[b] = np.einsum("hl,lhd->hd", weights, v)
+    return out, pool
+
+
+# ---------------------------------------------------------------------------
 # synthetic layers
 # ---------------------------------------------------------------------------
 

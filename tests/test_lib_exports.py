@@ -27,7 +27,8 @@ def _declared() -> list[str]:
 def test_header_declares_the_entry_points() -> None:
     names = _declared()
     for want in ("uocr_moe_int8_qmv", "uocr_moe_bf16_qmv", "uocr_int8_dequant_expert", "uocr_dense_bf16_qmv",
-                 "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward", "uocr_ngram_block"):
+                 "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward", "uocr_ngram_block",
+                 "uocr_paged_decode_attention", "uocr_paged_attention_workspace_bytes"):
         assert want in names
 
 
@@ -104,6 +105,30 @@ def test_ngram_refusals() -> None:
     ]
     for (rr, rv, lr, lv, hr, hl, nl), message in cases:
         assert _err("uocr_ngram_block", None, rr, rv, None, lr, lv, None, hr, hl, None, nl, None) == message
+
+
+def test_paged_attention_refusals_and_workspace_size() -> None:
+    """The host checks of uocr_paged_decode_attention, before anything is enqueued."""
+    from uocr_moe import _lib
+
+    def call(rows=1, heads=10, head_dim=128, pages=3, layers=2, page_size=128, layer=0, cols=2, attend_max=1):
+        return _err("uocr_paged_decode_attention", None, None, None, None, rows, heads, head_dim, None, pages, layers,
+                    page_size, layer, None, cols, None, attend_max, None, 1.0, None, 0, None)
+
+    assert call(head_dim=64) == "paged_decode_attention: head_dim must be 128, got 64"
+    assert call(page_size=64) == "paged_decode_attention: page_size must be a positive multiple of 128"
+    assert call(page_size=192) == "paged_decode_attention: page_size must be a positive multiple of 128"
+    assert call(layer=2) == "paged_decode_attention: layer 2 is not in the pool's 2 layers"
+    assert call(layer=-1) == "paged_decode_attention: layer -1 is not in the pool's 2 layers"
+    assert call(attend_max=257) == \
+        "paged_decode_attention: attend_max 257 is not in [1, 256], the rows the lookup table addresses"
+    assert call(attend_max=0).startswith("paged_decode_attention: attend_max 0 is not in")
+    assert call(rows=65536) == "paged_decode_attention: rows must be in [0, 65535] and heads in [1, 65535]"
+    assert call() == "paged_decode_attention: a tensor is missing"
+    lib = _lib.load()
+    assert lib.uocr_paged_attention_workspace_bytes(8, 10, 640) == 8 * 10 * 5 * 132 * 4
+    assert lib.uocr_paged_attention_workspace_bytes(1, 10, 129) == 10 * 2 * 132 * 4
+    assert lib.uocr_paged_attention_workspace_bytes(1, 10, 0) == 0
 
 
 def test_layer_refusals() -> None:

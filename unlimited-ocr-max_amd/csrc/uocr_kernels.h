@@ -162,6 +162,29 @@ constexpr int kNgramMaxHistory = 8192;
 hipError_t launch_ngram_block(float* result, const float* logits, int64_t rows, int64_t vocab,
                               const int32_t* history, int hist_len, const int32_t* ngram, hipStream_t s);
 
+// ---- paged decode attention (attention.hip) ----
+
+constexpr int kAttnSplitRows = 128;  // logical rows per partial workgroup (the page size is a multiple)
+struct PagedAttention {
+  float* out;            // [rows, heads, D]
+  const float* q;        // [rows, heads, D] post-RoPE
+  const float* k_new;    // [rows, heads, D] post-RoPE
+  const float* v_new;    // [rows, heads, D]
+  float* kv_blocks;      // [pages, 2, layers, page_size, heads, D]
+  int pages, layers, page_size, heads, head_dim, layer;
+  const uint32_t* lookup;       // [rows, lookup_cols]
+  int lookup_cols;
+  const uint32_t* write_index;     // [rows]
+  const uint32_t* attend_lengths;  // [rows], attend_len - 1 (the new row is one of attend_len)
+  int max_attend;                  // the largest attend_len (host)
+  int64_t rows;
+  float scale;
+  float* workspace;             // attn_workspace_bytes(rows, heads, max_attend)
+  uint32_t* counters;           // rows * heads words, zero between calls, or null (a second launch merges)
+};
+size_t attn_workspace_bytes(int64_t rows, int heads, int max_attend);
+hipError_t launch_paged_attention(const PagedAttention& p, hipStream_t s);
+
 // ---- the persistent decode layer (decode.hip) ----
 
 constexpr int kFusedWaves = 12;  // waves per workgroup, one workgroup per CU (168 VGPRs a lane)

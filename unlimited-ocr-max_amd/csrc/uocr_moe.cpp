@@ -404,6 +404,113 @@ int uocr_ngram_block(float* result, int64_t result_rows, int64_t result_vocab, c
   return e == hipSuccess ? 0 : hip_fail(err, errlen, "ngram_block", e);
 }
 
+// ------------------------------------------------------------------ paged decode attention
+
+// Counters of the attention's in-kernel merge of splits: per device,
+// kAttnSlots slots of kAttnCounters words, allocated and zeroed by the first
+// call on the device that is not under stream capture (until then calls merge
+// with a second launch); each stream takes a slot when first seen (round
+// robin), so streams first seen under capture need no allocation.  Every
+// launch leaves its counters zero.  Launches on streams that share a slot
+// must not overlap in time.
+static constexpr int64_t kAttnCounters = 65536;  // (row, head) pairs
+static constexpr int kAttnSlots = 16;
+struct AttnCounters {
+  uint32_t* words = nullptr;
+  int next = 0;
+  std::map<hipStream_t, int> slot;
+};
+static std::map<int, AttnCounters> g_attn_counters;
+
+static uint32_t* attn_counters(hipStream_t stream, int64_t pairs) {
+  if (pairs > kAttnCounters) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  AttnCounters& c = g_attn_counters[dev];
+  if (c.words == nullptr) {
+    if (capturing(stream)) return nullptr;
+    const int64_t words = kAttnSlots * kAttnCounters;
+    if (hipMalloc(&c.words, words * sizeof(uint32_t)) != hipSuccess) {
+      (void)hipGetLastError();
+      c.words = nullptr;
+      return nullptr;
+    }
+    // zeroed before any stream uses a slot
+    if (launch_zero_words(c.words, words, stream) != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) {
+      (void)hipGetLastError();
+      (void)hipFree(c.words);
+      c.words = nullptr;
+      return nullptr;
+    }
+  }
+  auto it = c.slot.find(stream);
+  const int k = it != c.slot.end() ? it->second : (c.slot[stream] = c.next++ % kAttnSlots);
+  return c.words + (int64_t)k * kAttnCounters;
+}
+
+size_t uocr_paged_attention_workspace_bytes(int64_t rows, int64_t heads, int64_t attend_max) {
+  if (rows < 0 || heads < 1 || attend_max < 1 || attend_max > INT32_MAX) return 0;
+  return attn_workspace_bytes(rows, (int)heads, (int)attend_max);
+}
+
+int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, const float* v_new, int64_t rows,
+                                int64_t heads, int64_t head_dim, float* kv_blocks, int64_t pages, int64_t layers,
+                                int64_t page_size, int64_t layer, const uint32_t* lookup, int64_t lookup_cols,
+                                const uint32_t* attend_lengths, int64_t attend_max, const uint32_t* write_index,
+                                float scale, void* workspace, size_t workspace_bytes, void* stream, char* err,
+                                size_t errlen) {
+  const char* op = "paged_decode_attention";
+  if (head_dim != 128) return fail(err, errlen, "%s: head_dim must be 128, got %lld", op, (long long)head_dim);
+  if (page_size < kAttnSplitRows || page_size % kAttnSplitRows)
+    return fail(err, errlen, "%s: page_size must be a positive multiple of %d", op, kAttnSplitRows);
+  if (pages < 1 || layers < 1 || layer < 0 || layer >= layers)
+    return fail(err, errlen, "%s: layer %lld is not in the pool's %lld layers", op, (long long)layer,
+                (long long)layers);
+  if (rows < 0 || rows > 65535 || heads < 1 || heads > 65535)
+    return fail(err, errlen, "%s: rows must be in [0, 65535] and heads in [1, 65535]", op);
+  if (lookup_cols < 1 || lookup_cols * page_size > INT32_MAX)
+    return fail(err, errlen, "%s: bad lookup table width %lld", op, (long long)lookup_cols);
+  if (attend_max < 1 || attend_max > lookup_cols * page_size)
+    return fail(err, errlen, "%s: attend_max %lld is not in [1, %lld], the rows the lookup table addresses", op,
+                (long long)attend_max, (long long)(lookup_cols * page_size));
+  if (pages > INT32_MAX) return fail(err, errlen, "%s: more than 2^31 pages", op);
+  if (rows == 0) return 0;
+  if (!out || !q || !k_new || !v_new || !kv_blocks || !lookup || !attend_lengths || !write_index)
+    return fail(err, errlen, "%s: a tensor is missing", op);
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!a16(out) || !a16(q) || !a16(k_new) || !a16(v_new) || !a16(kv_blocks) || !a16(workspace))
+    return fail(err, errlen, "%s: q, k_new, v_new, out, kv_blocks and workspace must be 16-byte aligned", op);
+  const hipStream_t s = (hipStream_t)stream;
+  void* ws = nullptr;
+  if (resolve_workspace(op, workspace, workspace_bytes, attn_workspace_bytes(rows, (int)heads, (int)attend_max), s,
+                        &ws, err, errlen))
+    return 1;
+  PagedAttention p{};
+  p.out = out;
+  p.q = q;
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.kv_blocks = kv_blocks;
+  p.pages = (int)pages;
+  p.layers = (int)layers;
+  p.page_size = (int)page_size;
+  p.heads = (int)heads;
+  p.head_dim = (int)head_dim;
+  p.layer = (int)layer;
+  p.lookup = lookup;
+  p.lookup_cols = (int)lookup_cols;
+  p.write_index = write_index;
+  p.attend_lengths = attend_lengths;
+  p.max_attend = (int)attend_max;
+  p.rows = rows;
+  p.scale = scale;
+  p.workspace = (float*)ws;
+  p.counters = attn_counters(s, rows * heads);
+  const hipError_t e = launch_paged_attention(p, s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
 // ------------------------------------------------------------------ the MoE block
 
 static int check_layer(const char* op, const uocr_moe_layer* L, int64_t hidden, char* err, size_t errlen) {
@@ -913,6 +1020,9 @@ void uocr_moe_release(void) {
   }
   g_fused.clear();
   g_fused_grid.clear();
+  for (auto& kv : g_attn_counters)
+    if (kv.second.words != nullptr) (void)hipFree(kv.second.words);
+  g_attn_counters.clear();
 }
 
 }  // extern "C"

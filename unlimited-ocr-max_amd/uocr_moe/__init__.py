@@ -2,13 +2,16 @@
 
 The product is the HIP library ``libuocr_moe.so`` behind a C ABI
 (``include/uocr_moe.h``); this package is its Python host side, mirroring the
-reference's op names (:mod:`uocr_moe.ops`) and MoE module (:mod:`uocr_moe.moe`).
+reference's op names (:mod:`uocr_moe.ops`) and MoE module (:mod:`uocr_moe.moe`),
+plus the ops either side of the block on the decode path (the paged decode
+attention, the dense lm_head GEMV, the n-gram guard).
 """
 
 from ._lib import LIB_PATH, UocrError
 from .checkpoint import WeightMappingError, load_safetensors, moe_from_checkpoint, moe_layer_weights
 from .moe import MoE, MoeConfig, gate
 from .ops import (
+    PagedKv,
     custom,
     dense_bf16_qmv,
     int8_dequant_expert,
@@ -16,6 +19,7 @@ from .ops import (
     moe_bf16_qmv,
     moe_int8_qmv,
     ngram_block,
+    paged_decode_attention,
     quantize_per_group,
 )
 
@@ -23,6 +27,7 @@ __all__ = [
     "LIB_PATH",
     "MoE",
     "MoeConfig",
+    "PagedKv",
     "UocrError",
     "WeightMappingError",
     "custom",
@@ -36,5 +41,6 @@ __all__ = [
     "moe_int8_qmv",
     "moe_layer_weights",
     "ngram_block",
+    "paged_decode_attention",
     "quantize_per_group",
 ]

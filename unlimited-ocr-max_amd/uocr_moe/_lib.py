@@ -49,6 +49,9 @@ SIGNATURES: dict[str, list] = {
                                  _vp, _cp, _sz],
     "uocr_dense_bf16_qmv": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _cp, _sz],
     "uocr_ngram_block": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _cp, _sz],
+    "uocr_paged_attention_workspace_bytes": [_i64, _i64, _i64],
+    "uocr_paged_decode_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i64,
+                                    _vp, _i64, _vp, ctypes.c_float, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_workspace_bytes": [ctypes.POINTER(Layer), _i64, _int],
     "uocr_moe_gate": [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _int, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_decode_rows": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],
@@ -59,7 +62,7 @@ SIGNATURES: dict[str, list] = {
     "uocr_moe_fused_trace": [_vp, _i64, ctypes.POINTER(_int), _cp, _sz],
     "uocr_moe_timing_end": [_int, _vp, _vp, _sz, ctypes.POINTER(_int), _cp, _sz],
 }
-_RESTYPES = {"uocr_moe_workspace_bytes": _sz, "uocr_moe_release": None}
+_RESTYPES = {"uocr_moe_workspace_bytes": _sz, "uocr_paged_attention_workspace_bytes": _sz, "uocr_moe_release": None}
 
 _LIB: ctypes.CDLL | None = None
 

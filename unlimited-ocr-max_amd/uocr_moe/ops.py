@@ -13,7 +13,11 @@ moe_bf16_qmv           x f32 [k,K], expert_ids i32 [k], w bf16 [E,N,K]      f32 
 int8_dequant_expert    w i8 [E,N,K], scales f32 [E,N,K/G], expert_idx i32   bf16 (or f32) [N,K]
                        [1]
 dense_bf16_qmv         x f32 [M,K], w bf16 [K/16,N,16]; parameter ``tile``  f32 [M,N]
+ngram_block            logits f32 [B,V], history i32 [B,W], ngram i32 [1]   f32 [B,V]
 =====================  ===================================================  ==================
+
+:func:`paged_decode_attention` (decoder.py:425-437) takes its page pool and
+step metadata as a :class:`PagedKv`.
 
 :func:`custom` dispatches by symbol like ``ops.custom(symbol, values=...)``.
 Inputs must be GPU tensors; non-contiguous views are packed first (the
@@ -24,6 +28,7 @@ enqueued on the current torch stream.
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -168,6 +173,76 @@ def ngram_block(logits, history, ngram, *, out: torch.Tensor | None = None) -> t
     orows = 1 if rank == 1 else int(out.shape[0])
     _lib.call("uocr_ngram_block", out.data_ptr(), orows, out.shape[-1], logits.data_ptr(), rows, logits.shape[-1],
               history.data_ptr(), hrows, history.shape[-1], ngram.data_ptr(), ngram.shape[0], _stream(logits))
+    return out
+
+
+@dataclass(frozen=True)
+class PagedKv:
+    """One decode step's view of the KV page pool: the pool and the step's metadata, as the reference's
+    ``PagedKv`` / ``PagedStep`` hold them (unlimited_ocr_max/decoder.py:407-422,
+    unlimited_ocr_max/kv_cache.py:169-207).
+
+    ``kv_blocks`` f32 ``[pages, 2, layers, page_size, heads, head_dim]`` (its last page the null page);
+    ``lookup_table`` ``[B, cols]``, ``attend_lengths`` ``[B]`` (``attend_len - 1``, the attention's cache
+    lengths) and ``write_index`` ``[B]`` (the store's), int32 or uint32 on the GPU; ``attend_max`` the
+    largest ``attend_len``, a host int.
+    """
+
+    kv_blocks: torch.Tensor
+    lookup_table: torch.Tensor
+    attend_lengths: torch.Tensor
+    attend_max: int
+    write_index: torch.Tensor
+
+
+def _u32(op: str, name: str, t: torch.Tensor, rank: int) -> torch.Tensor:
+    if isinstance(t, torch.Tensor) and t.dtype == torch.uint32:
+        return _gpu(op, name, t.view(torch.int32), torch.int32, rank)
+    return _gpu(op, name, t, torch.int32, rank)
+
+
+def paged_decode_attention(q, k_new, v_new, *, kv: PagedKv, layer_idx: int, scale: float,
+                           out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Store each row's new k/v at its write index, then attend each row over its own rows
+    (unlimited_ocr_max/decoder.py:425-437).
+
+    ``q`` / ``k_new`` / ``v_new`` are post-RoPE f32 ``[B, heads, head_dim]``, row ``b`` for request ``b``;
+    returns ``[B, heads, head_dim]``, row ``b`` attended over its logical rows ``[0, attend_lengths[b] + 1)``
+    of layer ``layer_idx``, logical row ``r`` being slot ``r % page_size`` of page
+    ``lookup_table[b, r // page_size]``.  ``kv.kv_blocks`` is written in place (it must be contiguous).
+    """
+    op = "paged_decode_attention"
+    q = _gpu(op, "q", q, torch.float32, 3)
+    k_new = _gpu(op, "k_new", k_new, torch.float32, 3)
+    v_new = _gpu(op, "v_new", v_new, torch.float32, 3)
+    if k_new.shape != q.shape or v_new.shape != q.shape:
+        raise ValueError(f"{op}: q, k_new and v_new disagree on shape: {tuple(q.shape)}, {tuple(k_new.shape)}, "
+                         f"{tuple(v_new.shape)}")
+    blocks = kv.kv_blocks
+    if not isinstance(blocks, torch.Tensor) or blocks.dtype != torch.float32 or blocks.dim() != 6:
+        raise ValueError(f"{op}: kv_blocks must be f32 [pages, 2, layers, page_size, heads, head_dim]")
+    if blocks.device.type != "cuda" or not blocks.is_contiguous():
+        raise ValueError(f"{op}: kv_blocks must be a contiguous GPU tensor (it is written in place)")
+    pages, two, layers, page_size, heads, head_dim = blocks.shape
+    rows = int(q.shape[0])
+    if two != 2 or (heads, head_dim) != tuple(q.shape[1:]):
+        raise ValueError(f"{op}: kv_blocks {tuple(blocks.shape)} does not hold [.., 2, .., .., heads, head_dim] "
+                         f"of q {tuple(q.shape)}")
+    lookup = _u32(op, "lookup_table", kv.lookup_table, 2)
+    attend = _u32(op, "attend_lengths", kv.attend_lengths, 1)
+    write = _u32(op, "write_index", kv.write_index, 1)
+    if lookup.shape[0] != rows or attend.shape[0] != rows or write.shape[0] != rows:
+        raise ValueError(f"{op}: the step metadata is not for {rows} rows")
+    if out is None:
+        out = torch.empty_like(q)
+    out = _gpu(op, "out", out, torch.float32, 3)
+    if out.shape != q.shape:
+        raise ValueError(f"{op}: out must be {tuple(q.shape)}, got {tuple(out.shape)}")
+    ws, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    _lib.call("uocr_paged_decode_attention", out.data_ptr(), q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), rows,
+              heads, head_dim, blocks.data_ptr(), pages, layers, page_size, int(layer_idx), lookup.data_ptr(),
+              lookup.shape[1], attend.data_ptr(), int(kv.attend_max), write.data_ptr(), float(scale), ws, ws_bytes,
+              _stream(q))
     return out
 
 
