@@ -119,6 +119,39 @@ int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, 
                                 const uint32_t* write_index, float scale, void* workspace,
                                 size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
+/* rms_norm -- replaces RmsNorm.__call__ (unlimited_ocr_max/decoder.py:252-261,
+ * ops.rms_norm with gamma cast to fp32) and, given `residual`, the residual add
+ * before it (DecoderLayer.decode, decoder.py:702-709).
+ *   x, residual, x_out, out fp32 [rows, dim]; gamma fp32 [dim].
+ *   v = x + residual (written to x_out, which may be x) or v = x;
+ *   out = (v * r) * gamma, r = 1 / sqrt(mean(v^2) + eps), fp32. */
+int uocr_rms_norm(float* out, float* x_out, const float* x, const float* residual, const float* gamma,
+                  int64_t rows, int64_t dim, float eps, void* stream, char* err, size_t errlen);
+
+/* rope -- replaces Attention._rope over the decode rows (decoder.py:459-462,
+ * 487-491) with rope_rows' gather (decoder.py:766-775).
+ *   q, k, v: [rows, heads, head_dim] fp32 views whose rows are in_row_stride
+ *   floats apart (e.g. the thirds of one fused q/k/v projection's output);
+ *   k and v may be NULL.  q_out, k_out, v_out fp32 [rows, heads, head_dim],
+ *   packed (an output may be its input when in_row_stride = heads * head_dim).
+ *   positions int32 [rows]; cos_table, sin_table fp32 [table_rows, head_dim]
+ *   (rope_tables, decoder.py:115-123), all device.
+ *   q_out, k_out = x * cos[pos] + rotate_half(x) * sin[pos], rotate_half(x) =
+ *   concat(-x[D/2:], x[:D/2]), both products and the sum rounded to fp32;
+ *   v_out = v.  A position outside [0, table_rows) is clamped into it. */
+int uocr_rope(float* q_out, float* k_out, float* v_out, const float* q, const float* k, const float* v,
+              int64_t rows, int64_t heads, int64_t head_dim, int64_t in_row_stride, const int32_t* positions,
+              const float* cos_table, const float* sin_table, int64_t table_rows, int64_t table_dim,
+              void* stream, char* err, size_t errlen);
+
+/* swiglu -- replaces ops.silu(gate) * up of GatedMlp.decode_rows
+ * (decoder.py:274-276) over one gate+up projection's output.
+ *   gate_up fp32 [rows, 2 * ffn] (gate columns, then up); out fp32 [rows, ffn];
+ *   out = silu(gate) * up, silu(g) = g / (1 + exp(-g)), each step rounded to
+ *   fp32 (the MoE kernels' silu). */
+int uocr_swiglu(float* out, const float* gate_up, int64_t rows, int64_t ffn, void* stream, char* err,
+                size_t errlen);
+
 /* dense_bf16_qmv -- replaces DenseBf16Qmv.execute[tile]
  * (unlimited_ocr_max/kernels/dense_bf16.mojo:119-158; staged by
  * dense_bf16_qmv, unlimited_ocr_max/decoder.py:166-184).

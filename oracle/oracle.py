@@ -533,6 +533,51 @@ def paged_decode_attention(q, k_new, v_new, kv_blocks, lookup, attend_lengths, w
 
 
 # ---------------------------------------------------------------------------
+# the decoder layer's per-row steps (unlimited_ocr_max/decoder.py)
+# ---------------------------------------------------------------------------
+
+
+def rms_norm(x, gamma, eps: float, residual=None) -> tuple[np.ndarray, np.ndarray]:
+    """``(out float64, v float32)``: ``v = x + residual`` in fp32 (or ``x``), then ``RmsNorm``
+    (decoder.py:252-261) in float64: ``v / sqrt(mean(v^2) + eps) * gamma``."""
+    v = np.asarray(x, np.float32)
+    if residual is not None:
+        v = (v + np.asarray(residual, np.float32)).astype(np.float32)
+    v64 = v.astype(np.float64)
+    r = 1.0 / np.sqrt(np.mean(v64 * v64, axis=-1, keepdims=True) + eps)
+    return v64 * r * np.asarray(gamma, np.float64), v
+
+
+def rope_tables(*, head_dim: int, seq_len: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
+    """``(cos, sin) [seq_len, head_dim]`` in float32 as the reference builds them (decoder.py:115-123):
+    inverse frequencies ``1 / theta^(2i/D)``, angles ``position * inv_freq``, duplicated halves."""
+    exponent = np.arange(0, head_dim, 2, dtype=np.int64).astype(np.float32)
+    inv_freq = (1.0 / (np.float32(theta) ** (exponent / np.float32(head_dim)))).astype(np.float32)
+    angles = np.arange(seq_len, dtype=np.int64).astype(np.float32)[:, None] * inv_freq[None, :]
+    emb = np.concatenate([angles, angles], axis=-1).astype(np.float32)
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+
+
+def rope(x, positions, cos_t, sin_t) -> np.ndarray:
+    """``Attention._rope`` (decoder.py:459-462) on ``x [rows, heads, D]`` with row ``b`` at
+    ``positions[b]``: ``x * cos + rotate_half(x) * sin`` in float32, each product and the sum rounded
+    (numpy's elementwise float32)."""
+    x = np.asarray(x, np.float32)
+    half = x.shape[-1] // 2
+    rotated = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    c = np.asarray(cos_t, np.float32)[np.asarray(positions)][:, None, :]
+    s = np.asarray(sin_t, np.float32)[np.asarray(positions)][:, None, :]
+    return (x * c + rotated * s).astype(np.float32)
+
+
+def swiglu(gate_up) -> np.ndarray:
+    """``silu(gate) * up`` (decoder.py:274-276) over ``[rows, 2F]``, with the oracle's fp32 silu."""
+    gu = np.asarray(gate_up, np.float32)
+    f = gu.shape[-1] // 2
+    return (silu_array(np.ascontiguousarray(gu[..., :f])) * gu[..., f:]).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
 # synthetic layers
 # ---------------------------------------------------------------------------
 

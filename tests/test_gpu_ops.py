@@ -302,5 +302,9 @@ def test_custom_dispatch(ops, oracle) -> None:
     x, ids, w, s = _rand_int8(3)
     [out] = ops.custom("moe_int8_qmv", values=[t(x), t(ids), t(w), t(s)])
     assert bits_equal(n(out), oracle.moe_int8_qmv(x, ids, w, s))
+    logits = np.random.default_rng(4).standard_normal((2, 64)).astype(np.float32)
+    hist = np.array([[1, 2, 3, 1, 2], [5, 6, 7, 8, 9]], np.int32)
+    [guarded] = ops.custom("ngram_block", values=[t(logits), t(hist), t(np.array([3], np.int32))])
+    assert np.array_equal(n(guarded), oracle.ngram_block(logits, hist, 3))
     with pytest.raises(KeyError):
-        ops.custom("ngram_block", values=[])
+        ops.custom("flash_attention_ragged", values=[])

@@ -28,7 +28,8 @@ def test_header_declares_the_entry_points() -> None:
     names = _declared()
     for want in ("uocr_moe_int8_qmv", "uocr_moe_bf16_qmv", "uocr_int8_dequant_expert", "uocr_dense_bf16_qmv",
                  "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward", "uocr_ngram_block",
-                 "uocr_paged_decode_attention", "uocr_paged_attention_workspace_bytes"):
+                 "uocr_paged_decode_attention", "uocr_paged_attention_workspace_bytes", "uocr_rms_norm", "uocr_rope",
+                 "uocr_swiglu"):
         assert want in names
 
 
@@ -129,6 +130,26 @@ def test_paged_attention_refusals_and_workspace_size() -> None:
     assert lib.uocr_paged_attention_workspace_bytes(8, 10, 640) == 8 * 10 * 5 * 132 * 4
     assert lib.uocr_paged_attention_workspace_bytes(1, 10, 129) == 10 * 2 * 132 * 4
     assert lib.uocr_paged_attention_workspace_bytes(1, 10, 0) == 0
+
+
+def test_decoder_step_refusals() -> None:
+    """The host checks of uocr_rms_norm, uocr_rope and uocr_swiglu, before anything is enqueued."""
+    assert _err("uocr_rms_norm", None, None, None, None, None, 2, 0, 1e-6, None) == "rms_norm: bad shape [2, 0]"
+    assert _err("uocr_rms_norm", None, None, None, None, None, 2, 8, -1.0, None) == "rms_norm: eps must be >= 0"
+    assert _err("uocr_rms_norm", None, None, None, None, None, 2, 8, 1e-6, None) == \
+        "rms_norm: a tensor is missing"
+
+    def rope(heads=2, head_dim=8, stride=16, table_rows=4, table_dim=8):
+        return _err("uocr_rope", None, None, None, None, None, None, 3, heads, head_dim, stride, None, None, None,
+                    table_rows, table_dim, None)
+
+    assert rope(head_dim=7, table_dim=7) == "rope: head_dim must be even for RoPE"
+    assert rope(table_dim=16) == "rope: the cos/sin tables are 16 wide, not head_dim 8"
+    assert rope(stride=15) == "rope: input rows 15 floats apart overlap rows of 16"
+    assert rope(table_rows=0) == "rope: bad shape"
+    assert rope() == "rope: a tensor is missing"
+    assert _err("uocr_swiglu", None, None, 2, 0, None) == "swiglu: bad shape [2, 0]"
+    assert _err("uocr_swiglu", None, None, 2, 4, None) == "swiglu: a tensor is missing"
 
 
 def test_layer_refusals() -> None:

@@ -19,7 +19,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "uocr_moe" / "libuocr_moe.so"
-SOURCES = ["gemv.hip", "route.hip", "gemm.hip", "decode.hip", "ngram.hip", "attention.hip", "uocr_moe.cpp"]
+SOURCES = ["gemv.hip", "route.hip", "gemm.hip", "decode.hip", "ngram.hip", "attention.hip", "decoder.hip", "uocr_moe.cpp"]
 ARCH = os.environ.get("UOCR_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [

@@ -162,6 +162,21 @@ constexpr int kNgramMaxHistory = 8192;
 hipError_t launch_ngram_block(float* result, const float* logits, int64_t rows, int64_t vocab,
                               const int32_t* history, int hist_len, const int32_t* ngram, hipStream_t s);
 
+// ---- the decoder layer's per-row steps (decoder.hip) ----
+
+// out = rmsnorm(x + delta) * gamma per row of `dim`; x + delta is written to
+// x_out (may be x).  delta null: out = rmsnorm(x) * gamma, x_out unused.
+hipError_t launch_add_rmsnorm(float* out, float* x_out, const float* x, const float* delta, const float* gamma,
+                              int64_t rows, int dim, float eps, hipStream_t s);
+// rotate_half RoPE of q and k [rows, heads, head_dim] (k may be null) at each
+// row's position, and a copy of v (may be null); input rows are in_stride
+// floats apart, outputs packed; an output may alias its input when packed.
+hipError_t launch_rope(float* q_out, float* k_out, float* v_out, const float* q, const float* k, const float* v,
+                       int64_t rows, int heads, int head_dim, int64_t in_stride, const int32_t* positions,
+                       const float* cos_t, const float* sin_t, int table_rows, hipStream_t s);
+// out [rows, ffn] = silu(gate_up[:, :ffn]) * gate_up[:, ffn:].
+hipError_t launch_swiglu(float* out, const float* gate_up, int64_t rows, int ffn, hipStream_t s);
+
 // ---- paged decode attention (attention.hip) ----
 
 constexpr int kAttnSplitRows = 128;  // logical rows per partial workgroup (the page size is a multiple)

@@ -404,6 +404,54 @@ int uocr_ngram_block(float* result, int64_t result_rows, int64_t result_vocab, c
   return e == hipSuccess ? 0 : hip_fail(err, errlen, "ngram_block", e);
 }
 
+// ------------------------------------------------------------------ the decoder layer's per-row steps
+
+int uocr_rms_norm(float* out, float* x_out, const float* x, const float* residual, const float* gamma, int64_t rows,
+                  int64_t dim, float eps, void* stream, char* err, size_t errlen) {
+  const char* op = "rms_norm";
+  if (rows < 0 || rows > INT32_MAX || dim < 1 || dim > INT32_MAX)
+    return fail(err, errlen, "%s: bad shape [%lld, %lld]", op, (long long)rows, (long long)dim);
+  if (!(eps >= 0.0f)) return fail(err, errlen, "%s: eps must be >= 0", op);
+  if (rows == 0) return 0;
+  if (!out || !x || !gamma || (residual && !x_out)) return fail(err, errlen, "%s: a tensor is missing", op);
+  const hipError_t e = launch_add_rmsnorm(out, x_out, x, residual, gamma, rows, (int)dim, eps, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+int uocr_rope(float* q_out, float* k_out, float* v_out, const float* q, const float* k, const float* v, int64_t rows,
+              int64_t heads, int64_t head_dim, int64_t in_row_stride, const int32_t* positions,
+              const float* cos_table, const float* sin_table, int64_t table_rows, int64_t table_dim, void* stream,
+              char* err, size_t errlen) {
+  const char* op = "rope";
+  if (head_dim < 2 || head_dim % 2) return fail(err, errlen, "%s: head_dim must be even for RoPE", op);
+  if (table_dim != head_dim)
+    return fail(err, errlen, "%s: the cos/sin tables are %lld wide, not head_dim %lld", op, (long long)table_dim,
+                (long long)head_dim);
+  if (rows < 0 || heads < 1 || table_rows < 1 || table_rows > INT32_MAX || head_dim > INT32_MAX ||
+      heads > INT32_MAX || rows * heads * head_dim > ((int64_t)1 << 31))
+    return fail(err, errlen, "%s: bad shape", op);
+  if (in_row_stride < heads * head_dim)
+    return fail(err, errlen, "%s: input rows %lld floats apart overlap rows of %lld", op, (long long)in_row_stride,
+                (long long)(heads * head_dim));
+  if (rows == 0) return 0;
+  if (!q || !q_out || !positions || !cos_table || !sin_table || (k && !k_out) || (v && !v_out))
+    return fail(err, errlen, "%s: a tensor is missing", op);
+  const hipError_t e = launch_rope(q_out, k_out, v_out, q, k, v, rows, (int)heads, (int)head_dim, in_row_stride,
+                                   positions, cos_table, sin_table, (int)table_rows, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+int uocr_swiglu(float* out, const float* gate_up, int64_t rows, int64_t ffn, void* stream, char* err,
+                size_t errlen) {
+  const char* op = "swiglu";
+  if (rows < 0 || ffn < 1 || ffn > INT32_MAX || rows * ffn > ((int64_t)1 << 31))
+    return fail(err, errlen, "%s: bad shape [%lld, %lld]", op, (long long)rows, (long long)ffn);
+  if (rows == 0) return 0;
+  if (!out || !gate_up) return fail(err, errlen, "%s: a tensor is missing", op);
+  const hipError_t e = launch_swiglu(out, gate_up, rows, (int)ffn, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
 // ------------------------------------------------------------------ paged decode attention
 
 // Counters of the attention's in-kernel merge of splits: per device,

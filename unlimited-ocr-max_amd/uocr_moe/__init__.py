@@ -3,12 +3,14 @@
 The product is the HIP library ``libuocr_moe.so`` behind a C ABI
 (``include/uocr_moe.h``); this package is its Python host side, mirroring the
 reference's op names (:mod:`uocr_moe.ops`) and MoE module (:mod:`uocr_moe.moe`),
-plus the ops either side of the block on the decode path (the paged decode
-attention, the dense lm_head GEMV, the n-gram guard).
+plus the ops either side of the block on the decode path (RMSNorm, RoPE, the
+paged decode attention, the dense projections and lm_head GEMV, the n-gram
+guard) and the decode step they make up (:mod:`uocr_moe.decoder`).
 """
 
 from ._lib import LIB_PATH, UocrError
 from .checkpoint import WeightMappingError, load_safetensors, moe_from_checkpoint, moe_layer_weights
+from .decoder import Decoder, DecoderConfig, DecoderLayer, rope_tables
 from .moe import MoE, MoeConfig, gate
 from .ops import (
     PagedKv,
@@ -21,9 +23,15 @@ from .ops import (
     ngram_block,
     paged_decode_attention,
     quantize_per_group,
+    rms_norm,
+    rope,
+    swiglu,
 )
 
 __all__ = [
+    "Decoder",
+    "DecoderConfig",
+    "DecoderLayer",
     "LIB_PATH",
     "MoE",
     "MoeConfig",
@@ -43,4 +51,8 @@ __all__ = [
     "ngram_block",
     "paged_decode_attention",
     "quantize_per_group",
+    "rms_norm",
+    "rope",
+    "rope_tables",
+    "swiglu",
 ]

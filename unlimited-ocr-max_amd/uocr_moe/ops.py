@@ -176,6 +176,100 @@ def ngram_block(logits, history, ngram, *, out: torch.Tensor | None = None) -> t
     return out
 
 
+def rms_norm(x, gamma, eps: float, *, residual=None, out: torch.Tensor | None = None,
+             x_out: torch.Tensor | None = None):
+    """``RmsNorm`` (unlimited_ocr_max/decoder.py:252-261) over the rows of ``x [rows, dim]`` with an fp32
+    ``gamma [dim]``.  Given ``residual``, the residual add before it (decoder.py:702-709):
+    ``v = x + residual`` is written to ``x_out`` (default: ``x`` itself, in place) and the norm of ``v``
+    is returned.  ``x`` must then be contiguous."""
+    op = "rms_norm"
+    if residual is not None and not x.is_contiguous():
+        raise ValueError(f"{op}: x must be contiguous when the residual is added in place")
+    x = _gpu(op, "x", x, torch.float32, 2)
+    gamma = _gpu(op, "gamma", gamma, torch.float32, 1)
+    if gamma.shape[0] != x.shape[1]:
+        raise ValueError(f"{op}: gamma has {gamma.shape[0]} entries for rows of {x.shape[1]}")
+    if residual is not None:
+        residual = _gpu(op, "residual", residual, torch.float32, 2)
+        if residual.shape != x.shape:
+            raise ValueError(f"{op}: residual {tuple(residual.shape)} and x {tuple(x.shape)} disagree")
+        x_out = x if x_out is None else _gpu(op, "x_out", x_out, torch.float32, 2)
+        if x_out.shape != x.shape or not x_out.is_contiguous():
+            raise ValueError(f"{op}: x_out must be a contiguous {tuple(x.shape)} tensor")
+    if out is None:
+        out = torch.empty_like(x)
+    out = _gpu(op, "out", out, torch.float32, 2)
+    if out.shape != x.shape:
+        raise ValueError(f"{op}: out must be {tuple(x.shape)}")
+    _lib.call("uocr_rms_norm", out.data_ptr(), _ptr(x_out), x.data_ptr(), _ptr(residual), gamma.data_ptr(),
+              x.shape[0], x.shape[1], float(eps), _stream(x))
+    return out
+
+
+def _rows_view(op: str, name: str, t, like=None) -> torch.Tensor:
+    """A ``[rows, heads, D]`` fp32 GPU view whose heads and elements are packed (rows may be strided)."""
+    if not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or t.dim() != 3 or t.device.type != "cuda":
+        raise ValueError(f"{op}: {name} must be an fp32 [rows, heads, head_dim] GPU tensor")
+    if t.stride(2) != 1 or t.stride(1) != t.shape[2]:
+        t = t.contiguous()
+    if like is not None and (t.shape != like.shape or t.stride(0) != like.stride(0)):
+        raise ValueError(f"{op}: {name} {tuple(t.shape)} (row stride {t.stride(0)}) does not match "
+                         f"{tuple(like.shape)} (row stride {like.stride(0)})")
+    return t
+
+
+def rope(q, k, positions, cos_table, sin_table, *, v=None, q_out=None, k_out=None, v_out=None):
+    """``Attention._rope`` on the decode rows (decoder.py:459-462,487-491) with the cos / sin rows gathered
+    at ``positions`` (``rope_rows``, decoder.py:766-775): ``q``, ``k`` ``[rows, heads, head_dim]`` (``k``
+    may be ``None``; rows may be strided, as the thirds of one fused q/k/v projection are), ``positions``
+    int32 ``[rows]``, tables ``[table_rows, head_dim]``.  ``v``, when given, is copied to a packed
+    ``v_out``.  Returns ``(q_out, k_out, v_out)``, packed; ``q_out=q`` rotates a packed ``q`` in place."""
+    op = "rope"
+    q = _rows_view(op, "q", q)
+    k = None if k is None else _rows_view(op, "k", k, q)
+    v = None if v is None else _rows_view(op, "v", v, q)
+    positions = _gpu(op, "positions", positions, torch.int32, 1)
+    if positions.shape[0] != q.shape[0]:
+        raise ValueError(f"{op}: {positions.shape[0]} positions for {q.shape[0]} rows")
+    cos_table = _gpu(op, "cos_table", cos_table, torch.float32, 2)
+    sin_table = _gpu(op, "sin_table", sin_table, torch.float32, 2)
+    if cos_table.shape != sin_table.shape:
+        raise ValueError(f"{op}: the cos and sin tables disagree on shape")
+    shape = tuple(q.shape)
+
+    def packed(name, t, src):
+        if src is None:
+            return None
+        t = torch.empty(shape, device=q.device, dtype=torch.float32) if t is None else t
+        if not isinstance(t, torch.Tensor) or tuple(t.shape) != shape or not t.is_contiguous() or \
+                t.dtype != torch.float32:
+            raise ValueError(f"{op}: {name} must be a contiguous fp32 {shape} tensor")
+        return t
+
+    q_out, k_out, v_out = packed("q_out", q_out, q), packed("k_out", k_out, k), packed("v_out", v_out, v)
+    _lib.call("uocr_rope", q_out.data_ptr(), _ptr(k_out), _ptr(v_out), q.data_ptr(), _ptr(k), _ptr(v), shape[0],
+              shape[1], shape[2], q.stride(0), positions.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+              cos_table.shape[0], cos_table.shape[1], _stream(q))
+    return q_out, k_out, v_out
+
+
+def swiglu(gate_up, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` of ``GatedMlp.decode_rows`` (decoder.py:274-276) over one gate+up projection's
+    output ``[rows, 2 * ffn]`` (gate columns first); returns ``[rows, ffn]``."""
+    op = "swiglu"
+    gate_up = _gpu(op, "gate_up", gate_up, torch.float32, 2)
+    if gate_up.shape[1] % 2:
+        raise ValueError(f"{op}: gate_up must hold 2 * ffn columns, got {gate_up.shape[1]}")
+    ffn = gate_up.shape[1] // 2
+    if out is None:
+        out = torch.empty((gate_up.shape[0], ffn), device=gate_up.device, dtype=torch.float32)
+    out = _gpu(op, "out", out, torch.float32, 2)
+    if tuple(out.shape) != (gate_up.shape[0], ffn):
+        raise ValueError(f"{op}: out must be {(gate_up.shape[0], ffn)}")
+    _lib.call("uocr_swiglu", out.data_ptr(), gate_up.data_ptr(), gate_up.shape[0], ffn, _stream(gate_up))
+    return out
+
+
 @dataclass(frozen=True)
 class PagedKv:
     """One decode step's view of the KV page pool: the pool and the step's metadata, as the reference's
