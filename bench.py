@@ -307,6 +307,72 @@ def bench_attention(device: str, rows: int, attend: int = 640, layers: int = 12,
             "partial_hbm_frac": round(nbytes / (part_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def bench_decoder_step(layers_w, B: int, device: str, steps: int = 20, attend: int = 640) -> dict:
+    """The whole decode step (uocr_moe.Decoder.decode + lm_head) at the served shapes: 12 layers of 10 x 128
+    attention over the paged pool (8 requests x 5 pages + the null page), layer 0's dense 6848 FFN, the 11
+    int8 MoE layers built for the decode lines, lm_head 129 280.  B requests attend `attend` rows and append
+    at row attend - 1.  `steps` decode steps in one graph, each from the same input hidden state."""
+    import torch
+    import uocr_moe
+
+    hid, heads, hd, ffn, vocab, n_layers, page = H, 10, 128, 6848, 129280, LAYERS + 1, 128
+    g = torch.Generator(device=device).manual_seed(777)
+
+    def kb(n_out, k_in):
+        w = (torch.randn((n_out, k_in), generator=g, device=device) * 0.02).to(torch.bfloat16)
+        return uocr_moe.kblocked(w)
+
+    w = {}
+    for i in range(n_layers):
+        p = f"layers.{i}."
+        for c in "qkvo":
+            w[f"{p}self_attn.{c}_proj.weight"] = kb(hid, hid)
+        w[p + "input_layernorm.weight"] = 1 + 0.1 * torch.randn(hid, generator=g, device=device)
+        w[p + "post_attention_layernorm.weight"] = 1 + 0.1 * torch.randn(hid, generator=g, device=device)
+        if i == 0:
+            w[p + "mlp.gate_proj.weight"], w[p + "mlp.up_proj.weight"] = kb(ffn, hid), kb(ffn, hid)
+            w[p + "mlp.down_proj.weight"] = kb(hid, ffn)
+        else:
+            w.update({f"{p}mlp.{k}": v for k, v in layers_w[i - 1][1].items()})
+    w["norm.weight"] = 1 + 0.1 * torch.randn(hid, generator=g, device=device)
+    w["lm_head.weight"] = kb(vocab, hid)
+    cfg = uocr_moe.DecoderConfig(hidden_size=hid, num_attention_heads=heads, num_hidden_layers=n_layers,
+                                 intermediate_size=ffn, first_k_dense_replace=1, vocab_size=vocab,
+                                 moe=layers_w[0][0].config)
+    dec = uocr_moe.Decoder(cfg, w, max_seq_len=2048)
+    per = (attend + page - 1) // page
+    pages = 8 * per + 1
+    pool = torch.randn((pages, 2, n_layers, page, heads, hd), generator=g, device=device)
+    order = torch.randperm(pages - 1, generator=torch.Generator().manual_seed(2)).to(torch.int32)
+    lut = torch.full((B, per + 1), pages - 1, dtype=torch.int32)
+    lut[:, :per] = order[: B * per].reshape(B, per)
+    kv = uocr_moe.PagedKv(kv_blocks=pool, lookup_table=lut.to(device),
+                          attend_lengths=torch.full((B,), attend - 1, dtype=torch.int32, device=device),
+                          attend_max=attend, write_index=torch.full((B,), attend - 1, dtype=torch.int32,
+                                                                    device=device))
+    positions = torch.full((B,), attend - 1, dtype=torch.int32, device=device)
+    base = rmsnorm_rows(g, B, device)
+    hidden = torch.empty_like(base)
+    moe_ws = layers_w[0][0].workspace(B, prefill=False)
+    from uocr_moe import _lib
+
+    attn_ws = torch.empty(_lib.load().uocr_paged_attention_workspace_bytes(B, heads, attend) // 4, device=device)
+    out = {}
+
+    def step():
+        hidden.copy_(base)
+        out["logits"] = dec.logits_rows(dec.decode(hidden, positions=positions, kv=kv, moe_workspace=moe_ws,
+                                                   attn_workspace=attn_ws))
+
+    us = time_graph(graph_of([step] * steps)) * 1e3 / steps
+    ok = bool(torch.isfinite(out["logits"]).all())
+    del dec, w, pool, kv
+    torch.cuda.empty_cache()
+    return {"rows": B, "layers": n_layers, "attend": attend, "us_per_step": round(us, 2),
+            "tokens_per_s": round(B / (us * 1e-6), 1), "steps_in_graph": steps, "finite": ok,
+            "step": "12 x (norm, q/k/v, RoPE, paged attention, o_proj, norm, dense FFN or int8 MoE), norm, lm_head"}
+
+
 def zipf_prefill_inputs(g, T: int, device: str, seed: int):
     """274 vision + 238 text rows of N(0,1) (per 512); a constant feature carries a Zipf(1.1) expert bias."""
     import torch
@@ -531,6 +597,10 @@ def main() -> int:
             "steps_in_graph": args.steps // LAYERS, "layers": LAYERS,
             "inputs": "an independent RMS-normalised batch per layer launch"}
     if not args.quick:
+        for B in (1, 8):
+            log(f"decode step, 12 layers + lm_head, B={B}")
+            results[f"decoder_step_b{B}"] = bench_decoder_step(layers_w, B, dev)
+            log(f"  {results[f'decoder_step_b{B}']}")
         log("prefill int8 T=512 (Zipf)")
         results["prefill_int8_t512"] = bench_prefill(layers_w, 512, dev, 512)
         log(f"  {results['prefill_int8_t512']['tflops']} TFLOP/s")

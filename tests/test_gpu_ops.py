@@ -248,7 +248,7 @@ def _rand_dense(oracle, seed, m, n_, k):
 
 
 @pytest.mark.parametrize(("m", "n_", "k"), [(1, 24, 64), (5, 24, 64), (8, 40, 96), (13, 7, 32), (9, 1792, 1280),
-                                            (3, 1280, 1792)])
+                                            (3, 1280, 1792), (2, 3840, 1280), (1, 129, 6848), (2, 1280, 6848)])
 def test_dense_every_tile(ops, oracle, m, n_, k) -> None:
     x, w = _rand_dense(oracle, m * 1000 + n_ + k, m, n_, k)
     want = oracle.dense_bf16_qmv_chunked(x, w)

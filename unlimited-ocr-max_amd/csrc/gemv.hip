@@ -277,7 +277,134 @@ __global__ void __launch_bounds__(kGemvMaxThreads) k_gemv1(GemvArgs a) {
   gemv_part<W, NPROJ>(a, (int)blockIdx.x, lds);
 }
 
+// ---------------------------------------------------------------------------
+// dense_bf16_qmv for narrow outputs (N < kDenseNarrowMaxN) and at most
+// kDenseNarrowMaxRows rows (past 2 rows the activation reads from LDS, 32 per
+// row and chunk, cost more than k_gemv1's scalar loads).  k_gemv1 gives a
+// workgroup 64 output columns (lane = column, wave = chunk), so a 1280-wide
+// projection runs on 20 workgroups.  Here a lane is a (column, chunk) pair: a
+// workgroup holds kNarrowCols columns x kNarrowSlots chunks (256 lanes), so
+// N = 1280 gets 80 workgroups.  Each lane runs the same chain as chunk_chain
+// (fma over the chunk's k in ascending order, from 0), the partials meet in
+// LDS, and thread (row, column) adds them in chunk order from 0 -- the bits of
+// k_gemv1.  The activations of a batch of chunks are staged in LDS (a chunk's
+// 128 floats, padded to 132 so that the 4 chunks a wave reads at once sit in
+// different banks), since a wave now spans 4 chunks.
+constexpr int kNarrowCols = 16;
+constexpr int kNarrowThreads = 256;
+constexpr int kNarrowSlots = kNarrowThreads / kNarrowCols;  // chunks per batch
+constexpr int kNarrowPitch = kChunk + 4;
+
+template <int R>
+__device__ __attribute__((always_inline)) void dense_narrow_tile(const GemvArgs& a, int t, int cnt, int n0,
+                                                                 float* xs, float* fold) {
+  const int tid = (int)threadIdx.x;
+  const int c = tid % kNarrowCols, j = tid / kNarrowCols;
+  const int n = min(n0 + c, a.N - 1);
+  const uint16_t* w = (const uint16_t*)a.p[0].w;
+  // the fold thread (row fr, column fc) keeps its sum across batches
+  const int fr = tid / kNarrowCols, fc = tid % kNarrowCols;
+  float acc = 0.0f;
+  for (int cb = 0; cb < a.nchunks; cb += kNarrowSlots) {
+    const int nb = min(kNarrowSlots, a.nchunks - cb);
+    // stage x rows t .. t+R-1 (padded rows repeat the last real row) for chunks cb .. cb+nb-1
+    for (int i = tid; i < R * nb * kChunk; i += kNarrowThreads) {
+      const int r = i / (nb * kChunk);
+      const int rem = i - r * nb * kChunk;
+      const int ch = rem / kChunk, kk = rem - ch * kChunk;
+      const int64_t k = (int64_t)(cb + ch) * kChunk + kk;
+      const int row = t + min(r, cnt - 1);
+      xs[(r * kNarrowSlots + ch) * kNarrowPitch + kk] = k < a.K ? ldg(a.x + (int64_t)row * a.ldx + k) : 0.0f;
+    }
+    __syncthreads();
+    float part[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[r] = 0.0f;
+    if (j < nb) {
+      const int64_t k0 = (int64_t)(cb + j) * kChunk;
+      const int len = (int)min((int64_t)kChunk, (int64_t)a.K - k0);
+      const float* xj = xs + j * kNarrowPitch;
+      if (a.vec && len == kChunk) {
+        int4 buf[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t kk = k0 + i * 8;
+          buf[i] = load_nt16(w + ((kk >> 4) * a.N + n) * 16 + (kk & 15));
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const f32x4 x0 = *(const f32x4*)(xj + r * kNarrowSlots * kNarrowPitch + i * 8);
+            const f32x4 x1 = *(const f32x4*)(xj + r * kNarrowSlots * kNarrowPitch + i * 8 + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t word =
+                  (uint32_t)(q == 0 ? buf[i].x : q == 1 ? buf[i].y : q == 2 ? buf[i].z : buf[i].w);
+              part[r] = __builtin_fmaf(bf16_lo(word), xv[2 * q], part[r]);
+              part[r] = __builtin_fmaf(bf16_hi(word), xv[2 * q + 1], part[r]);
+            }
+          }
+        }
+      } else {
+        for (int i = 0; i < len; ++i) {
+          const int64_t kk = k0 + i;
+          const float wv = bf16_bits_to_f32(ldg(w + ((kk >> 4) * a.N + n) * 16 + (kk & 15)));
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            part[r] = __builtin_fmaf(wv, xj[r * kNarrowSlots * kNarrowPitch + i], part[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) fold[(r * kNarrowSlots + j) * kNarrowCols + c] = part[r];
+    __syncthreads();
+    if (fr < R) {
+      for (int jj = 0; jj < nb; ++jj) acc = acc + fold[(fr * kNarrowSlots + jj) * kNarrowCols + fc];
+    }
+    __syncthreads();  // xs and fold are rewritten by the next batch
+  }
+  if (fr < cnt && n0 + fc < a.N) stg(a.out + (int64_t)(t + fr) * a.ldo + n0 + fc, acc);
+}
+
+__global__ void __launch_bounds__(kNarrowThreads) k_dense_narrow(GemvArgs a) {
+  extern __shared__ float lds[];
+  float* fold = lds;                                           // [8][slots][cols]
+  float* xs = lds + 8 * kNarrowSlots * kNarrowCols;            // [R][slots][pitch]
+  const int n0 = (int)blockIdx.x * kNarrowCols;
+  const int rows = a.rows.identity;
+  for (int t = 0; t < rows; t += 8) {
+    const int cnt = min(8, rows - t);
+    if (cnt == 1)
+      dense_narrow_tile<1>(a, t, cnt, n0, xs, fold);
+    else if (cnt == 2)
+      dense_narrow_tile<2>(a, t, cnt, n0, xs, fold);
+    else if (cnt <= 4)
+      dense_narrow_tile<4>(a, t, cnt, n0, xs, fold);
+    else
+      dense_narrow_tile<8>(a, t, cnt, n0, xs, fold);
+  }
+}
+
 }  // namespace
+
+hipError_t launch_dense(const GemvArgs& a, int waves, hipStream_t s) {
+  if (a.N >= kDenseNarrowMaxN || a.rows.identity > kDenseNarrowMaxRows || a.kind != kBf16KBlocked ||
+      a.rows.n_groups != nullptr)
+    return launch_gemv(a, 1, 1, waves, s);
+  if (a.N == 0 || a.rows.identity == 0) return hipSuccess;
+  const int rows = a.rows.identity;
+  const int rmax = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+  const size_t lds = (size_t)(8 * kNarrowSlots * kNarrowCols + rmax * kNarrowSlots * kNarrowPitch) * sizeof(float);
+  // 8 rows need 74 KB of LDS, past the default limit of a launch
+  static const hipError_t attr = hipFuncSetAttribute((const void*)k_dense_narrow,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+  if (attr != hipSuccess) return attr;
+  UOCR_LAUNCH("dense_narrow", k_dense_narrow, dim3((unsigned)((a.N + kNarrowCols - 1) / kNarrowCols)),
+              dim3(kNarrowThreads), lds, s, a);
+  return hipGetLastError();
+}
 
 int gemv_workgroups(const GemvArgs& a, int max_groups) {
   const int cols = (a.N + kWave - 1) / kWave;

@@ -69,6 +69,12 @@ constexpr int kGemvMaxWaves = 10;
 constexpr int kGemvMaxThreads = kGemvMaxWaves * 64;
 constexpr int kGemvMaxBatch = 16;
 
+// dense_bf16_qmv: below kDenseNarrowMaxN output columns and for at most
+// kDenseNarrowMaxRows rows, a (column, chunk) lane mapping (16 columns a
+// workgroup, the same bits); else launch_gemv.
+constexpr int kDenseNarrowMaxN = 16384;
+constexpr int kDenseNarrowMaxRows = 2;
+hipError_t launch_dense(const GemvArgs& a, int waves, hipStream_t s);
 int gemv_workgroups(const GemvArgs& a, int max_groups);
 size_t gemv_lds_bytes(int batch, int nproj);
 hipError_t launch_gemv(const GemvArgs& a, int max_groups, int nproj, int waves, hipStream_t s);

@@ -379,7 +379,7 @@ int uocr_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n, const
   a.vec = aligned16(w);
   a.batch = batch_for(a.nchunks);
   a.rows = Rows{nullptr, nullptr, nullptr, nullptr, (int)x_m};
-  const hipError_t e = launch_gemv(a, 1, 1, waves_for(a.batch), (hipStream_t)stream);
+  const hipError_t e = launch_dense(a, waves_for(a.batch), (hipStream_t)stream);
   return e == hipSuccess ? 0 : hip_fail(err, errlen, "dense_bf16_qmv", e);
 }
 
