@@ -119,6 +119,23 @@ int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, 
                                 const uint32_t* write_index, float scale, void* workspace,
                                 size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
+/* paged_decode_attention_qkv -- Attention.decode's RoPE and paged_decode_attention
+ * in one launch (unlimited_ocr_max/decoder.py:487-492 with :425-437): the same op
+ * as uocr_paged_decode_attention, whose q / k_new / v_new are here the thirds of
+ * one fused projection's output, qkv [rows, 3, heads, head_dim] with rows
+ * row_stride floats apart, q and k_new before RoPE.  q and the new k row are
+ * rotated in the kernel exactly as uocr_rope does (the stored k row and the
+ * output have the bits of uocr_rope followed by uocr_paged_decode_attention);
+ * positions int32 [rows], cos_table / sin_table fp32 [table_rows, head_dim]. */
+int uocr_paged_decode_attention_qkv(float* out, const float* qkv, int64_t rows, int64_t heads, int64_t head_dim,
+                                    int64_t row_stride, const int32_t* positions, const float* cos_table,
+                                    const float* sin_table, int64_t table_rows, int64_t table_dim,
+                                    float* kv_blocks, int64_t pages, int64_t layers, int64_t page_size,
+                                    int64_t layer, const uint32_t* lookup, int64_t lookup_cols,
+                                    const uint32_t* attend_lengths, int64_t attend_max,
+                                    const uint32_t* write_index, float scale, void* workspace,
+                                    size_t workspace_bytes, void* stream, char* err, size_t errlen);
+
 /* rms_norm -- replaces RmsNorm.__call__ (unlimited_ocr_max/decoder.py:252-261,
  * ops.rms_norm with gamma cast to fp32) and, given `residual`, the residual add
  * before it (DecoderLayer.decode, decoder.py:702-709).

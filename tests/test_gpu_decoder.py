@@ -65,6 +65,43 @@ def test_rope_from_a_fused_qkv_buffer(oracle) -> None:
     assert np.array_equal(n(inplace), n(q))
 
 
+@pytest.mark.parametrize("B", [1, 3])
+def test_attention_with_rope_in_the_kernel_equals_rope_then_attention(oracle, B) -> None:
+    """``paged_decode_attention_qkv`` (RoPE of q and k inside the attention kernel, read from a fused
+    projection's output) gives the bits of ``rope`` followed by ``paged_decode_attention``: the output and
+    every pool word."""
+    uocr = _ops()
+    rng = np.random.default_rng(30 + B)
+    H, D, P, layers, seq = 10, 128, 128, 2, 1024
+    cos_t, sin_t = oracle.rope_tables(head_dim=D, seq_len=seq, theta=10000.0)
+    pages = 4 * B + 1
+    pool = rng.standard_normal((pages, 2, layers, P, H, D)).astype(np.float32)
+    perm = rng.permutation(pages - 1)
+    lut = np.full((B, 5), pages - 1, np.uint32)
+    lut[:, :4] = perm[: 4 * B].reshape(B, 4)
+    attend = np.array([300, 129, 512][:B], np.uint32)
+    write = np.array([299, 60, 511][:B], np.uint32)  # appends and a ring overwrite
+    pos = np.array([299, 900, 511][:B], np.int32)
+    # the fused projection's output, rows 64 floats wider than q, k and v (a strided view)
+    g = t(rng.standard_normal((B, 3 * H * D + 64)).astype(np.float32))[:, : 3 * H * D]
+
+    def kv_of(gpu_pool):
+        return uocr.PagedKv(kv_blocks=gpu_pool, lookup_table=t(lut.view(np.int32)),
+                            attend_lengths=t((attend - 1).view(np.int32)), attend_max=int(attend.max()),
+                            write_index=t(write.view(np.int32)))
+
+    cos_g, sin_g, pos_g = t(cos_t), t(sin_t), t(pos)
+    two = t(pool)
+    q, k, v = uocr.rope(g[:, : H * D].view(B, H, D), g[:, H * D: 2 * H * D].view(B, H, D), pos_g, cos_g, sin_g,
+                        v=g[:, 2 * H * D:].view(B, H, D))
+    want = n(uocr.paged_decode_attention(q, k, v, kv=kv_of(two), layer_idx=1, scale=1 / math.sqrt(D)))
+    one = t(pool)
+    got = n(uocr.paged_decode_attention_qkv(g, pos_g, cos_g, sin_g, heads=H, kv=kv_of(one), layer_idx=1,
+                                            scale=1 / math.sqrt(D)))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(n(one).view(np.uint32), n(two).view(np.uint32))
+
+
 def test_swiglu(oracle) -> None:
     rng = np.random.default_rng(6)
     gu = (4 * rng.standard_normal((8, 2 * 6848))).astype(np.float32)

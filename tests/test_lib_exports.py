@@ -29,7 +29,7 @@ def test_header_declares_the_entry_points() -> None:
     for want in ("uocr_moe_int8_qmv", "uocr_moe_bf16_qmv", "uocr_int8_dequant_expert", "uocr_dense_bf16_qmv",
                  "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward", "uocr_ngram_block",
                  "uocr_paged_decode_attention", "uocr_paged_attention_workspace_bytes", "uocr_rms_norm", "uocr_rope",
-                 "uocr_swiglu"):
+                 "uocr_swiglu", "uocr_paged_decode_attention_qkv"):
         assert want in names
 
 
@@ -148,6 +148,13 @@ def test_decoder_step_refusals() -> None:
     assert rope(stride=15) == "rope: input rows 15 floats apart overlap rows of 16"
     assert rope(table_rows=0) == "rope: bad shape"
     assert rope() == "rope: a tensor is missing"
+    def qkv(stride=3840, table_dim=128, rows=1):
+        return _err("uocr_paged_decode_attention_qkv", None, None, rows, 10, 128, stride, None, None, None, 16,
+                    table_dim, None, 3, 2, 128, 0, None, 2, None, 1, None, 1.0, None, 0, None)
+
+    assert qkv(stride=3839) == "paged_decode_attention_qkv: qkv rows 3839 floats apart overlap rows of 3840"
+    assert qkv(table_dim=64) == "paged_decode_attention_qkv: the cos/sin tables are 64 wide, not head_dim 128"
+    assert qkv() == "paged_decode_attention_qkv: a tensor is missing"
     assert _err("uocr_swiglu", None, None, 2, 0, None) == "swiglu: bad shape [2, 0]"
     assert _err("uocr_swiglu", None, None, 2, 4, None) == "swiglu: a tensor is missing"
 

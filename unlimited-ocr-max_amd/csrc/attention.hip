@@ -52,7 +52,36 @@ struct PagedArgs {
   int lookup_cols;
   const uint32_t* write_index;
   const uint32_t* attend_lengths;  // attend_len - 1 per row
+  int64_t in_stride;               // floats between rows of q / k_new / v_new
+  const int32_t* positions;        // null: q and k_new come rotated; else RoPE them at these positions
+  const float* cos_t;
+  const float* sin_t;
+  int table_rows;
 };
+
+// RoPE of the pair (x[d], x[d + 64]) with cos / sin rows c, s: each product
+// and the sum rounded to fp32, no contraction (the bits of k_rope).
+__device__ __forceinline__ void rope_pair(float& lo, float& hi, const float* c, const float* s, int d) {
+#pragma clang fp contract(off)
+  const float l = lo, h = hi;
+  lo = l * ldg(c + d) - h * ldg(s + d);
+  hi = h * ldg(c + d + kD / 2) + l * ldg(s + d + kD / 2);
+}
+__device__ __forceinline__ void rope_pair4(f32x4& lo, f32x4& hi, const float* c, const float* s, int d) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float l = lo[e], h = hi[e];
+    rope_pair(l, h, c, s, d + e);
+    lo[e] = l;
+    hi[e] = h;
+  }
+}
+// Element d of the rotated row x.
+__device__ __forceinline__ float rope_elem(const float* x, const float* c, const float* s, int d) {
+  float lo = ldg(x + (d % (kD / 2))), hi = ldg(x + (d % (kD / 2)) + kD / 2);
+  rope_pair(lo, hi, c, s, d % (kD / 2));
+  return d < kD / 2 ? lo : hi;
+}
 
 // Pointer to the k (kv = 0) or v (kv = 1) values of logical row r of batch row b, head h.
 __device__ __forceinline__ float* row_ptr(const PagedArgs& a, int b, int h, int r, int kv) {
@@ -129,23 +158,39 @@ __device__ __forceinline__ void split_partial(const PagedArgs& a, const float* _
   const int n = r1 - r0;
   const int sub = tid % kLanesPerRow, rg = tid / kLanesPerRow;
   const int c = tid % (kD / 4), g = tid / (kD / 4);
-  const float* qh = q + bh * kD + sub * 4;
+  const int64_t qoff = (int64_t)b * a.in_stride + (int64_t)h * kD;  // row b, head h of q / k_new / v_new
+  const float* qh = q + qoff + sub * 4;
+  const float* rc = nullptr;
+  const float* rs = nullptr;
+  if (a.positions != nullptr) {
+    const int pos = min(max(ldg(a.positions + b), 0), a.table_rows - 1);  // device data: clamped into the table
+    rc = a.cos_t + (int64_t)pos * kD;
+    rs = a.sin_t + (int64_t)pos * kD;
+  }
   const float* kbase = split_base(a, b, h, r0, 0);
   const float* vbase = split_base(a, b, h, r0, 1);
   f32x4 qv[4], kv[kKRows][4], vv[kVRows];
 #pragma unroll
   for (int u = 0; u < 4; ++u) qv[u] = *(const UOCR_GLOBAL f32x4*)(qh + 32 * u);
+  if (rc != nullptr) {  // lane elements d = sub*4 + 32u + e: u = 0, 1 pair with u = 2, 3
+    rope_pair4(qv[0], qv[2], rc, rs, sub * 4);
+    rope_pair4(qv[1], qv[3], rc, rs, 32 + sub * 4);
+  }
 #pragma unroll
   for (int j = 0; j < kKRows; ++j) {
     const int i = rg + j * kRowsPerPass;
-    const float* kr = (r0 + i == w_idx ? k_new + bh * kD : kbase + (int64_t)i * a.slot_stride) + sub * 4;
+    const float* kr = (r0 + i == w_idx ? k_new + qoff : kbase + (int64_t)i * a.slot_stride) + sub * 4;
 #pragma unroll
     for (int u = 0; u < 4; ++u) kv[j][u] = *(const UOCR_GLOBAL f32x4*)(kr + 32 * u);
+    if (rc != nullptr && r0 + i == w_idx) {  // the new row, read unrotated
+      rope_pair4(kv[j][0], kv[j][2], rc, rs, sub * 4);
+      rope_pair4(kv[j][1], kv[j][3], rc, rs, 32 + sub * 4);
+    }
   }
 #pragma unroll
   for (int j = 0; j < kVRows; ++j) {
     const int i = g + j * kValueGroups;
-    const float* vr = r0 + i == w_idx ? v_new + bh * kD : vbase + (int64_t)i * a.slot_stride;
+    const float* vr = r0 + i == w_idx ? v_new + qoff : vbase + (int64_t)i * a.slot_stride;
     vv[j] = *(const UOCR_GLOBAL f32x4*)(vr + 4 * c);
   }
   // ---- scores
@@ -244,9 +289,17 @@ __global__ void __launch_bounds__(kThreads) k_attn_partial(PagedArgs a, const fl
   float* dst = part + (bh * splits + s) * kPart;
   if (s == 0 && w_idx >= 0) {
     // the new row into the pool (its readers in this launch take it from k_new / v_new)
+    const int64_t qoff = (int64_t)b * a.in_stride + (int64_t)h * kD;
     for (int i = tid; i < 2 * kD; i += kThreads) {
       const int kv = i / kD, d = i % kD;
-      row_ptr(a, b, h, w_idx, kv)[d] = ldg((kv ? v_new : k_new) + bh * kD + d);
+      float v;
+      if (kv == 0 && a.positions != nullptr) {
+        const int pos = min(max(ldg(a.positions + b), 0), a.table_rows - 1);
+        v = rope_elem(k_new + qoff, a.cos_t + (int64_t)pos * kD, a.sin_t + (int64_t)pos * kD, d);
+      } else {
+        v = ldg((kv ? v_new : k_new) + qoff + d);
+      }
+      row_ptr(a, b, h, w_idx, kv)[d] = v;
     }
   }
   if (r0 >= r1) {  // nothing to attend in this split: an empty partial
@@ -298,6 +351,11 @@ hipError_t launch_paged_attention(const PagedAttention& p, hipStream_t s) {
   a.lookup_cols = p.lookup_cols;
   a.write_index = p.write_index;
   a.attend_lengths = p.attend_lengths;
+  a.in_stride = p.in_stride > 0 ? p.in_stride : (int64_t)p.heads * kD;
+  a.positions = p.positions;
+  a.cos_t = p.cos_table;
+  a.sin_t = p.sin_table;
+  a.table_rows = p.table_rows;
   const int splits = (p.max_attend + kAttnSplitRows - 1) / kAttnSplitRows;
   const dim3 grid((unsigned)(splits > 0 ? splits : 1), (unsigned)p.heads, (unsigned)p.rows);
   UOCR_LAUNCH("attn_partial", k_attn_partial, grid, dim3(kThreads), 0, s, a, p.q, p.k_new, p.v_new, p.scale,

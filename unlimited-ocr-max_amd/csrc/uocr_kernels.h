@@ -202,6 +202,11 @@ struct PagedAttention {
   float scale;
   float* workspace;             // attn_workspace_bytes(rows, heads, max_attend)
   uint32_t* counters;           // rows * heads words, zero between calls, or null (a second launch merges)
+  int64_t in_stride;            // floats between rows of q / k_new / v_new (0: heads * head_dim, packed)
+  const int32_t* positions;     // null: q, k_new are post-RoPE; else rotated here at these positions
+  const float* cos_table;       // [table_rows, head_dim]
+  const float* sin_table;
+  int table_rows;
 };
 size_t attn_workspace_bytes(int64_t rows, int heads, int max_attend);
 hipError_t launch_paged_attention(const PagedAttention& p, hipStream_t s);

@@ -502,13 +502,15 @@ size_t uocr_paged_attention_workspace_bytes(int64_t rows, int64_t heads, int64_t
   return attn_workspace_bytes(rows, (int)heads, (int)attend_max);
 }
 
-int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, const float* v_new, int64_t rows,
-                                int64_t heads, int64_t head_dim, float* kv_blocks, int64_t pages, int64_t layers,
-                                int64_t page_size, int64_t layer, const uint32_t* lookup, int64_t lookup_cols,
+// The checks and launch of both paged attention entries.
+static int paged_attention_call(const char* op, float* out, const float* q, const float* k_new, const float* v_new,
+                                int64_t in_stride, const int32_t* positions, const float* cos_table,
+                                const float* sin_table, int64_t table_rows, int64_t rows, int64_t heads,
+                                int64_t head_dim, float* kv_blocks, int64_t pages, int64_t layers, int64_t page_size,
+                                int64_t layer, const uint32_t* lookup, int64_t lookup_cols,
                                 const uint32_t* attend_lengths, int64_t attend_max, const uint32_t* write_index,
                                 float scale, void* workspace, size_t workspace_bytes, void* stream, char* err,
                                 size_t errlen) {
-  const char* op = "paged_decode_attention";
   if (head_dim != 128) return fail(err, errlen, "%s: head_dim must be 128, got %lld", op, (long long)head_dim);
   if (page_size < kAttnSplitRows || page_size % kAttnSplitRows)
     return fail(err, errlen, "%s: page_size must be a positive multiple of %d", op, kAttnSplitRows);
@@ -527,7 +529,7 @@ int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, 
   if (!out || !q || !k_new || !v_new || !kv_blocks || !lookup || !attend_lengths || !write_index)
     return fail(err, errlen, "%s: a tensor is missing", op);
   const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  if (!a16(out) || !a16(q) || !a16(k_new) || !a16(v_new) || !a16(kv_blocks) || !a16(workspace))
+  if (!a16(out) || !a16(q) || !a16(k_new) || !a16(v_new) || !a16(kv_blocks) || !a16(workspace) || in_stride % 4)
     return fail(err, errlen, "%s: q, k_new, v_new, out, kv_blocks and workspace must be 16-byte aligned", op);
   const hipStream_t s = (hipStream_t)stream;
   void* ws = nullptr;
@@ -555,8 +557,50 @@ int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, 
   p.scale = scale;
   p.workspace = (float*)ws;
   p.counters = attn_counters(s, rows * heads);
+  p.in_stride = in_stride;
+  p.positions = positions;
+  p.cos_table = cos_table;
+  p.sin_table = sin_table;
+  p.table_rows = (int)table_rows;
   const hipError_t e = launch_paged_attention(p, s);
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
+int uocr_paged_decode_attention(float* out, const float* q, const float* k_new, const float* v_new, int64_t rows,
+                                int64_t heads, int64_t head_dim, float* kv_blocks, int64_t pages, int64_t layers,
+                                int64_t page_size, int64_t layer, const uint32_t* lookup, int64_t lookup_cols,
+                                const uint32_t* attend_lengths, int64_t attend_max, const uint32_t* write_index,
+                                float scale, void* workspace, size_t workspace_bytes, void* stream, char* err,
+                                size_t errlen) {
+  return paged_attention_call("paged_decode_attention", out, q, k_new, v_new, heads * head_dim, nullptr, nullptr,
+                              nullptr, 0, rows, heads, head_dim, kv_blocks, pages, layers, page_size, layer, lookup,
+                              lookup_cols, attend_lengths, attend_max, write_index, scale, workspace,
+                              workspace_bytes, stream, err, errlen);
+}
+
+int uocr_paged_decode_attention_qkv(float* out, const float* qkv, int64_t rows, int64_t heads, int64_t head_dim,
+                                    int64_t row_stride, const int32_t* positions, const float* cos_table,
+                                    const float* sin_table, int64_t table_rows, int64_t table_dim, float* kv_blocks,
+                                    int64_t pages, int64_t layers, int64_t page_size, int64_t layer,
+                                    const uint32_t* lookup, int64_t lookup_cols, const uint32_t* attend_lengths,
+                                    int64_t attend_max, const uint32_t* write_index, float scale, void* workspace,
+                                    size_t workspace_bytes, void* stream, char* err, size_t errlen) {
+  const char* op = "paged_decode_attention_qkv";
+  if (table_dim != head_dim)
+    return fail(err, errlen, "%s: the cos/sin tables are %lld wide, not head_dim %lld", op, (long long)table_dim,
+                (long long)head_dim);
+  if (table_rows < 1 || table_rows > INT32_MAX) return fail(err, errlen, "%s: bad cos/sin table", op);
+  if (row_stride < 3 * heads * head_dim)
+    return fail(err, errlen, "%s: qkv rows %lld floats apart overlap rows of %lld", op, (long long)row_stride,
+                (long long)(3 * heads * head_dim));
+  if (rows > 0 && (!qkv || !positions || !cos_table || !sin_table))
+    return fail(err, errlen, "%s: a tensor is missing", op);
+  const float* k = qkv ? qkv + heads * head_dim : nullptr;
+  const float* v = qkv ? qkv + 2 * heads * head_dim : nullptr;
+  return paged_attention_call(op, out, qkv, k, v, row_stride, positions, cos_table, sin_table, table_rows, rows,
+                              heads, head_dim, kv_blocks, pages, layers, page_size, layer, lookup, lookup_cols,
+                              attend_lengths, attend_max, write_index, scale, workspace, workspace_bytes, stream, err,
+                              errlen);
 }
 
 // ------------------------------------------------------------------ the MoE block

@@ -22,6 +22,7 @@ from .ops import (
     moe_int8_qmv,
     ngram_block,
     paged_decode_attention,
+    paged_decode_attention_qkv,
     quantize_per_group,
     rms_norm,
     rope,
@@ -50,6 +51,7 @@ __all__ = [
     "moe_layer_weights",
     "ngram_block",
     "paged_decode_attention",
+    "paged_decode_attention_qkv",
     "quantize_per_group",
     "rms_norm",
     "rope",

@@ -6,8 +6,9 @@ Per layer, for ``B`` rows (one token of each of ``B`` requests):
 * ``input_layernorm`` (with the previous layer's residual add fused in: :func:`ops.rms_norm`);
 * one ``dense_bf16_qmv`` over the q, k and v projections at once (their K-blocked weights side by side
   along N, the reference's three ``Projection.decode_rows`` calls in one launch);
-* RoPE of q and k at each row's position, v made packed (:func:`ops.rope`);
-* :func:`ops.paged_decode_attention` (stores the new k/v rows, attends each row's own pages);
+* :func:`ops.paged_decode_attention_qkv`: RoPE of q and k at each row's position and the paged attention
+  (stores the new k/v rows, attends each row's own pages) in one launch, with the bits of
+  :func:`ops.rope` followed by :func:`ops.paged_decode_attention`;
 * ``o_proj``, then ``post_attention_layernorm`` with the attention residual fused in;
 * the MoE block (:meth:`uocr_moe.MoE.decode_rows`) or, for the first ``first_k_dense_replace`` layers,
   the dense gated MLP (one gate+up ``dense_bf16_qmv``, :func:`ops.swiglu`, ``down``).
@@ -93,12 +94,11 @@ class DecoderLayer:
         """``x [B, hidden]`` is the residual stream; ``delta`` the previous layer's output, added to ``x``
         in place before this layer's input norm.  Returns this layer's output (the next ``delta``)."""
         c = self.config
-        rows, heads, hd = x.shape[0], c.num_attention_heads, c.head_dim
+        rows, heads = x.shape[0], c.num_attention_heads
         normed = ops.rms_norm(x, self.input_norm, c.rms_norm_eps, residual=delta)
-        qkv = ops.dense_bf16_qmv(normed, self.qkv).view(rows, 3, heads, hd)
-        q, k_new, v_new = ops.rope(qkv[:, 0], qkv[:, 1], positions, cos, sin, v=qkv[:, 2])
-        attended = ops.paged_decode_attention(q, k_new, v_new, kv=kv, layer_idx=self.layer_idx, scale=scale,
-                                              workspace=attn_workspace)
+        qkv = ops.dense_bf16_qmv(normed, self.qkv)
+        attended = ops.paged_decode_attention_qkv(qkv, positions, cos, sin, heads=heads, kv=kv,
+                                                  layer_idx=self.layer_idx, scale=scale, workspace=attn_workspace)
         attn_out = ops.dense_bf16_qmv(attended.view(rows, c.hidden_size), self.o_proj)
         normed = ops.rms_norm(x, self.post_norm, c.rms_norm_eps, residual=attn_out)
         if self.moe is not None:

@@ -340,6 +340,50 @@ def paged_decode_attention(q, k_new, v_new, *, kv: PagedKv, layer_idx: int, scal
     return out
 
 
+def paged_decode_attention_qkv(qkv, positions, cos_table, sin_table, *, heads: int, kv: PagedKv, layer_idx: int,
+                               scale: float, out: torch.Tensor | None = None,
+                               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`rope` of q and k followed by :func:`paged_decode_attention`, in one launch and with the same
+    bits: ``qkv [B, 3 * heads * head_dim]`` (q, k, v side by side, q and k before RoPE; rows may be
+    strided) is one fused projection's output (unlimited_ocr_max/decoder.py:487-492 with :425-437)."""
+    op = "paged_decode_attention_qkv"
+    if not isinstance(qkv, torch.Tensor) or qkv.dtype != torch.float32 or qkv.dim() != 2 or qkv.device.type != "cuda":
+        raise ValueError(f"{op}: qkv must be an fp32 [rows, 3 * heads * head_dim] GPU tensor")
+    if qkv.stride(1) != 1:
+        qkv = qkv.contiguous()
+    rows, width = qkv.shape
+    if width % (3 * heads):
+        raise ValueError(f"{op}: qkv width {width} is not 3 x {heads} heads")
+    head_dim = width // (3 * heads)
+    positions = _gpu(op, "positions", positions, torch.int32, 1)
+    cos_table = _gpu(op, "cos_table", cos_table, torch.float32, 2)
+    sin_table = _gpu(op, "sin_table", sin_table, torch.float32, 2)
+    if positions.shape[0] != rows or cos_table.shape != sin_table.shape:
+        raise ValueError(f"{op}: positions or the cos/sin tables do not fit {rows} rows")
+    blocks = kv.kv_blocks
+    if not isinstance(blocks, torch.Tensor) or blocks.dtype != torch.float32 or blocks.dim() != 6 or \
+            blocks.device.type != "cuda" or not blocks.is_contiguous():
+        raise ValueError(f"{op}: kv_blocks must be a contiguous f32 [pages, 2, layers, page_size, heads, head_dim]")
+    pages, two, layers, page_size, bh, bd = blocks.shape
+    if two != 2 or (bh, bd) != (heads, head_dim):
+        raise ValueError(f"{op}: kv_blocks {tuple(blocks.shape)} does not hold {heads} heads of {head_dim}")
+    lookup = _u32(op, "lookup_table", kv.lookup_table, 2)
+    attend = _u32(op, "attend_lengths", kv.attend_lengths, 1)
+    write = _u32(op, "write_index", kv.write_index, 1)
+    if lookup.shape[0] != rows or attend.shape[0] != rows or write.shape[0] != rows:
+        raise ValueError(f"{op}: the step metadata is not for {rows} rows")
+    if out is None:
+        out = torch.empty((rows, heads, head_dim), device=qkv.device, dtype=torch.float32)
+    out = _gpu(op, "out", out, torch.float32, 3)
+    ws, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    _lib.call("uocr_paged_decode_attention_qkv", out.data_ptr(), qkv.data_ptr(), rows, heads, head_dim, qkv.stride(0),
+              positions.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0],
+              cos_table.shape[1], blocks.data_ptr(), pages, layers, page_size, int(layer_idx), lookup.data_ptr(),
+              lookup.shape[1], attend.data_ptr(), int(kv.attend_max), write.data_ptr(), float(scale), ws, ws_bytes,
+              _stream(qkv))
+    return out
+
+
 _OPS = {
     "moe_int8_qmv": moe_int8_qmv,
     "moe_bf16_qmv": moe_bf16_qmv,
