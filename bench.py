@@ -353,6 +353,7 @@ def bench_decoder_step(layers_w, B: int, device: str, steps: int = 20, attend: i
     positions = torch.full((B,), attend - 1, dtype=torch.int32, device=device)
     base = rmsnorm_rows(g, B, device)
     hidden = torch.empty_like(base)
+    scratch = torch.empty_like(base)
     moe_ws = layers_w[0][0].workspace(B, prefill=False)
     from uocr_moe import _lib
 
@@ -362,7 +363,7 @@ def bench_decoder_step(layers_w, B: int, device: str, steps: int = 20, attend: i
     def step():
         hidden.copy_(base)
         out["logits"] = dec.logits_rows(dec.decode(hidden, positions=positions, kv=kv, moe_workspace=moe_ws,
-                                                   attn_workspace=attn_ws))
+                                                   attn_workspace=attn_ws, scratch=scratch))
 
     us = time_graph(graph_of([step] * steps)) * 1e3 / steps
     ok = bool(torch.isfinite(out["logits"]).all())

@@ -145,6 +145,20 @@ int uocr_paged_decode_attention_qkv(float* out, const float* qkv, int64_t rows, 
 int uocr_rms_norm(float* out, float* x_out, const float* x, const float* residual, const float* gamma,
                   int64_t rows, int64_t dim, float eps, void* stream, char* err, size_t errlen);
 
+/* rms_norm_dense_bf16_qmv -- RmsNorm (with the residual add before it) and the
+ * dense_bf16_qmv that consumes it in one launch, for decode rows
+ * (DecoderLayer.decode's input_layernorm and q/k/v projections,
+ * decoder.py:702-709 with :487-491; the ops of uocr_rms_norm and
+ * uocr_dense_bf16_qmv, with their bits).
+ *   x fp32 [M, K] (M <= 2, K <= 2048), residual fp32 [M, K] or NULL, x_out fp32
+ *   [M, K] (x + residual; must not overlap x or residual), gamma fp32 [K],
+ *   w bf16 K-blocked [K/16, N, 16] (N < 16384), result fp32 [M, N] =
+ *   rmsnorm(x + residual) * gamma @ W^T. */
+int uocr_rms_norm_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n, const float* x, int64_t x_m,
+                                 int64_t x_kdim, const float* residual, float* x_out, const float* gamma, float eps,
+                                 const uint16_t* w, int64_t w_blocks, int64_t w_n, int64_t w_kblock, void* stream,
+                                 char* err, size_t errlen);
+
 /* rope -- replaces Attention._rope over the decode rows (decoder.py:459-462,
  * 487-491) with rope_rows' gather (decoder.py:766-775).
  *   q, k, v: [rows, heads, head_dim] fp32 views whose rows are in_row_stride

@@ -102,6 +102,28 @@ def test_attention_with_rope_in_the_kernel_equals_rope_then_attention(oracle, B)
     assert np.array_equal(n(one).view(np.uint32), n(two).view(np.uint32))
 
 
+@pytest.mark.parametrize("rows", [1, 2])
+@pytest.mark.parametrize("resid", [False, True])
+def test_norm_inside_the_projection_equals_norm_then_projection(oracle, rows, resid) -> None:
+    uocr = _ops()
+    rng = np.random.default_rng(40 + rows + resid)
+    x = rng.standard_normal((rows, 1280)).astype(np.float32)
+    d = rng.standard_normal((rows, 1280)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(1280)).astype(np.float32)
+    w = t(_bf16_kb(rng, 3840, 1280, 0.03))
+    x_out = torch.full((rows, 1280), float("nan"), device="cuda:0")
+    got = uocr.rms_norm_dense_bf16_qmv(t(x), t(g), 1e-6, w, residual=t(d) if resid else None,
+                                       x_out=x_out if resid else None)
+    xs = t(x)
+    want = uocr.dense_bf16_qmv(uocr.rms_norm(xs, t(g), 1e-6, residual=t(d) if resid else None), w)
+    assert np.array_equal(n(got).view(np.uint32), n(want).view(np.uint32))
+    if resid:
+        assert np.array_equal(n(x_out).view(np.uint32), n(xs).view(np.uint32))
+        with pytest.raises(uocr.UocrError, match="must not overlap"):
+            xg = t(x)
+            uocr.rms_norm_dense_bf16_qmv(xg, t(g), 1e-6, w, residual=t(d), x_out=xg)
+
+
 def test_swiglu(oracle) -> None:
     rng = np.random.default_rng(6)
     gu = (4 * rng.standard_normal((8, 2 * 6848))).astype(np.float32)
@@ -224,7 +246,12 @@ def test_decoder_decode_step_matches_the_oracle_chain(oracle) -> None:
         kv = uocr_moe.PagedKv(kv_blocks=gpu_pool, lookup_table=t(lut.view(np.int32)),
                               attend_lengths=t((attend - 1).view(np.int32)), attend_max=int(attend.max()),
                               write_index=t(write.view(np.int32)))
+        apart_pool = gpu_pool.clone()
+        apart = dec.decode(t(hidden), positions=t(pos), kv=uocr_moe.PagedKv(
+            kv_blocks=apart_pool, lookup_table=kv.lookup_table, attend_lengths=kv.attend_lengths,
+            attend_max=kv.attend_max, write_index=kv.write_index), fuse_norm=False)
         normed = dec.decode(t(hidden), positions=t(pos), kv=kv)
+        assert np.array_equal(n(normed).view(np.uint32), n(apart).view(np.uint32))  # the fused norms: same bits
         logits = dec.logits_rows(normed)
         want_n, want_l, pool = _oracle_step(oracle, w, moes, pool, lut, attend, write, pos, hidden, cos_t, sin_t)
         assert _rel(n(normed), want_n) <= 1e-4, (step, _rel(n(normed), want_n))

@@ -29,7 +29,7 @@ def test_header_declares_the_entry_points() -> None:
     for want in ("uocr_moe_int8_qmv", "uocr_moe_bf16_qmv", "uocr_int8_dequant_expert", "uocr_dense_bf16_qmv",
                  "uocr_moe_gate", "uocr_moe_decode_rows", "uocr_moe_forward", "uocr_ngram_block",
                  "uocr_paged_decode_attention", "uocr_paged_attention_workspace_bytes", "uocr_rms_norm", "uocr_rope",
-                 "uocr_swiglu", "uocr_paged_decode_attention_qkv"):
+                 "uocr_swiglu", "uocr_paged_decode_attention_qkv", "uocr_rms_norm_dense_bf16_qmv"):
         assert want in names
 
 
@@ -155,6 +155,15 @@ def test_decoder_step_refusals() -> None:
     assert qkv(stride=3839) == "paged_decode_attention_qkv: qkv rows 3839 floats apart overlap rows of 3840"
     assert qkv(table_dim=64) == "paged_decode_attention_qkv: the cos/sin tables are 64 wide, not head_dim 128"
     assert qkv() == "paged_decode_attention_qkv: a tensor is missing"
+    def nd(m=2, n=3840, k=1280, blocks=80):
+        return _err("uocr_rms_norm_dense_bf16_qmv", None, m, n, None, m, k, None, None, None, 1e-6, None, blocks, n,
+                    16, None)
+
+    assert nd(m=3) == "rms_norm_dense_bf16_qmv: takes at most 2 rows, N < 16384 and K <= 2048"
+    assert nd(n=16384) == "rms_norm_dense_bf16_qmv: takes at most 2 rows, N < 16384 and K <= 2048"
+    assert nd(k=4096, blocks=256) == "rms_norm_dense_bf16_qmv: takes at most 2 rows, N < 16384 and K <= 2048"
+    assert nd(blocks=79) == "rms_norm_dense_bf16_qmv: w and x disagree on K"
+    assert nd() == "rms_norm_dense_bf16_qmv: a tensor is missing"
     assert _err("uocr_swiglu", None, None, 2, 0, None) == "swiglu: bad shape [2, 0]"
     assert _err("uocr_swiglu", None, None, 2, 4, None) == "swiglu: a tensor is missing"
 

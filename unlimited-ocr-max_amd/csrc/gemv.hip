@@ -295,9 +295,51 @@ constexpr int kNarrowThreads = 256;
 constexpr int kNarrowSlots = kNarrowThreads / kNarrowCols;  // chunks per batch
 constexpr int kNarrowPitch = kChunk + 4;
 
+// The RMSNorm prologue of a fused call (rows of x replaced by rmsnorm(x + residual) * gamma before the
+// projection): the order of k_add_rmsnorm, so the normed rows have its bits.
+struct NormPrologue {
+  const float* residual;  // null: no residual add
+  float* x_out;           // x + residual, written by workgroup 0 (with a residual)
+  const float* gamma;
+  float eps;
+};
+
 template <int R>
-__device__ __attribute__((always_inline)) void dense_narrow_tile(const GemvArgs& a, int t, int cnt, int n0,
-                                                                 float* xs, float* fold) {
+__device__ __attribute__((always_inline)) void norm_staged(const GemvArgs& a, const NormPrologue& np, int t,
+                                                           int cnt, float* xs, float* red) {
+  const int tid = (int)threadIdx.x;
+  for (int r = 0; r < R; ++r) {
+    if (r >= cnt) break;  // padded rows are never stored
+    float* xr = xs + r * kNarrowSlots * kNarrowPitch;
+    float ss = 0.0f;
+    for (int k = tid; k < a.K; k += kNarrowThreads) {
+      const int idx = (k / kChunk) * kNarrowPitch + k % kChunk;
+      float v = xr[idx];
+      if (np.residual != nullptr) {
+        v = v + ldg(np.residual + (int64_t)(t + r) * a.ldx + k);
+        xr[idx] = v;
+        if (blockIdx.x == 0) np.x_out[(int64_t)(t + r) * a.ldx + k] = v;
+      }
+      ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = tree_sum(ss);
+    if (lane_id() == 0) red[tid / kWave] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();  // red is reused by the next row
+    const float rn = 1.0f / sqrtf(ss / (float)a.K + np.eps);
+    for (int k = tid; k < a.K; k += kNarrowThreads) {
+      const int idx = (k / kChunk) * kNarrowPitch + k % kChunk;
+      xr[idx] = (xr[idx] * rn) * ldg(np.gamma + k);
+    }
+  }
+  __syncthreads();
+}
+
+template <int R, bool NORM>
+__device__ __attribute__((always_inline)) void dense_narrow_tile(const GemvArgs& a, const NormPrologue& np, int t,
+                                                                 int cnt, int n0, float* xs, float* fold,
+                                                                 float* red) {
   const int tid = (int)threadIdx.x;
   const int c = tid % kNarrowCols, j = tid / kNarrowCols;
   const int n = min(n0 + c, a.N - 1);
@@ -317,6 +359,7 @@ __device__ __attribute__((always_inline)) void dense_narrow_tile(const GemvArgs&
       xs[(r * kNarrowSlots + ch) * kNarrowPitch + kk] = k < a.K ? ldg(a.x + (int64_t)row * a.ldx + k) : 0.0f;
     }
     __syncthreads();
+    if constexpr (NORM) norm_staged<R>(a, np, t, cnt, xs, red);  // the whole row is in this one batch
     float part[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) part[r] = 0.0f;
@@ -368,8 +411,10 @@ __device__ __attribute__((always_inline)) void dense_narrow_tile(const GemvArgs&
   if (fr < cnt && n0 + fc < a.N) stg(a.out + (int64_t)(t + fr) * a.ldo + n0 + fc, acc);
 }
 
-__global__ void __launch_bounds__(kNarrowThreads) k_dense_narrow(GemvArgs a) {
+template <bool NORM>
+__global__ void __launch_bounds__(kNarrowThreads) k_dense_narrow(GemvArgs a, NormPrologue np) {
   extern __shared__ float lds[];
+  __shared__ float red[kNarrowThreads / kWave];
   float* fold = lds;                                           // [8][slots][cols]
   float* xs = lds + 8 * kNarrowSlots * kNarrowCols;            // [R][slots][pitch]
   const int n0 = (int)blockIdx.x * kNarrowCols;
@@ -377,32 +422,48 @@ __global__ void __launch_bounds__(kNarrowThreads) k_dense_narrow(GemvArgs a) {
   for (int t = 0; t < rows; t += 8) {
     const int cnt = min(8, rows - t);
     if (cnt == 1)
-      dense_narrow_tile<1>(a, t, cnt, n0, xs, fold);
+      dense_narrow_tile<1, NORM>(a, np, t, cnt, n0, xs, fold, red);
     else if (cnt == 2)
-      dense_narrow_tile<2>(a, t, cnt, n0, xs, fold);
+      dense_narrow_tile<2, NORM>(a, np, t, cnt, n0, xs, fold, red);
     else if (cnt <= 4)
-      dense_narrow_tile<4>(a, t, cnt, n0, xs, fold);
+      dense_narrow_tile<4, NORM>(a, np, t, cnt, n0, xs, fold, red);
     else
-      dense_narrow_tile<8>(a, t, cnt, n0, xs, fold);
+      dense_narrow_tile<8, NORM>(a, np, t, cnt, n0, xs, fold, red);
   }
 }
 
 }  // namespace
+
+static size_t dense_narrow_lds(int rows) {
+  const int rmax = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+  return (size_t)(8 * kNarrowSlots * kNarrowCols + rmax * kNarrowSlots * kNarrowPitch) * sizeof(float);
+}
 
 hipError_t launch_dense(const GemvArgs& a, int waves, hipStream_t s) {
   if (a.N >= kDenseNarrowMaxN || a.rows.identity > kDenseNarrowMaxRows || a.kind != kBf16KBlocked ||
       a.rows.n_groups != nullptr)
     return launch_gemv(a, 1, 1, waves, s);
   if (a.N == 0 || a.rows.identity == 0) return hipSuccess;
-  const int rows = a.rows.identity;
-  const int rmax = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-  const size_t lds = (size_t)(8 * kNarrowSlots * kNarrowCols + rmax * kNarrowSlots * kNarrowPitch) * sizeof(float);
   // 8 rows need 74 KB of LDS, past the default limit of a launch
-  static const hipError_t attr = hipFuncSetAttribute((const void*)k_dense_narrow,
+  static const hipError_t attr = hipFuncSetAttribute((const void*)k_dense_narrow<false>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
   if (attr != hipSuccess) return attr;
-  UOCR_LAUNCH("dense_narrow", k_dense_narrow, dim3((unsigned)((a.N + kNarrowCols - 1) / kNarrowCols)),
-              dim3(kNarrowThreads), lds, s, a);
+  UOCR_LAUNCH("dense_narrow", k_dense_narrow<false>, dim3((unsigned)((a.N + kNarrowCols - 1) / kNarrowCols)),
+              dim3(kNarrowThreads), dense_narrow_lds(a.rows.identity), s, a, NormPrologue{});
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_dense(const GemvArgs& a, const float* residual, float* x_out, const float* gamma, float eps,
+                             hipStream_t s) {
+  if (a.N >= kDenseNarrowMaxN || a.rows.identity > kDenseNarrowMaxRows || a.kind != kBf16KBlocked ||
+      a.K > kNarrowSlots * kChunk || a.rows.n_groups != nullptr)
+    return hipErrorInvalidValue;
+  if (a.N == 0 || a.rows.identity == 0) return hipSuccess;
+  static const hipError_t attr = hipFuncSetAttribute((const void*)k_dense_narrow<true>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+  if (attr != hipSuccess) return attr;
+  UOCR_LAUNCH("norm_dense", k_dense_narrow<true>, dim3((unsigned)((a.N + kNarrowCols - 1) / kNarrowCols)),
+              dim3(kNarrowThreads), dense_narrow_lds(a.rows.identity), s, a, NormPrologue{residual, x_out, gamma, eps});
   return hipGetLastError();
 }
 

@@ -75,6 +75,11 @@ constexpr int kGemvMaxBatch = 16;
 constexpr int kDenseNarrowMaxN = 16384;
 constexpr int kDenseNarrowMaxRows = 2;
 hipError_t launch_dense(const GemvArgs& a, int waves, hipStream_t s);
+// The same narrow projection of rmsnorm(x + residual) * gamma (x + residual
+// written to x_out when residual is given), normed in LDS with the order of
+// the standalone RMSNorm kernel: at most kDenseNarrowMaxRows rows, K <= 2048.
+hipError_t launch_norm_dense(const GemvArgs& a, const float* residual, float* x_out, const float* gamma, float eps,
+                             hipStream_t s);
 int gemv_workgroups(const GemvArgs& a, int max_groups);
 size_t gemv_lds_bytes(int batch, int nproj);
 hipError_t launch_gemv(const GemvArgs& a, int max_groups, int nproj, int waves, hipStream_t s);

@@ -406,6 +406,53 @@ int uocr_ngram_block(float* result, int64_t result_rows, int64_t result_vocab, c
 
 // ------------------------------------------------------------------ the decoder layer's per-row steps
 
+int uocr_rms_norm_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n, const float* x, int64_t x_m,
+                                 int64_t x_kdim, const float* residual, float* x_out, const float* gamma, float eps,
+                                 const uint16_t* w, int64_t w_blocks, int64_t w_n, int64_t w_kblock, void* stream,
+                                 char* err, size_t errlen) {
+  const char* op = "rms_norm_dense_bf16_qmv";
+  if (result_m != x_m) return fail(err, errlen, "%s: x and output disagree on M", op);
+  if (w_n != result_n) return fail(err, errlen, "%s: w and output disagree on N", op);
+  if (w_kblock != 16) return fail(err, errlen, "%s: w is not K-blocked by KBLOCK", op);
+  if (w_blocks * 16 != x_kdim) return fail(err, errlen, "%s: w and x disagree on K", op);
+  if (x_m < 0 || x_m > kDenseNarrowMaxRows || result_n < 1 || result_n >= kDenseNarrowMaxN || x_kdim < 1 ||
+      x_kdim > 2048)
+    return fail(err, errlen, "%s: takes at most %d rows, N < %d and K <= 2048", op, kDenseNarrowMaxRows,
+                kDenseNarrowMaxN);
+  if (!(eps >= 0.0f)) return fail(err, errlen, "%s: eps must be >= 0", op);
+  if (x_m == 0) return 0;
+  if (!result || !x || !gamma || !w || (residual && !x_out)) return fail(err, errlen, "%s: a tensor is missing", op);
+  if (residual) {
+    const auto overlap = [&](const void* p) {
+      const char* a0 = (const char*)x_out;
+      const char* b0 = (const char*)p;
+      const size_t bytes = (size_t)(x_m * x_kdim) * sizeof(float);
+      return a0 < b0 + bytes && b0 < a0 + bytes;
+    };
+    if (overlap(x) || overlap(residual))
+      return fail(err, errlen, "%s: x_out must not overlap x or residual (workgroups read them while one writes)",
+                  op);
+  }
+  GemvArgs a{};
+  a.out = result;
+  a.ldo = result_n;
+  a.x = x;
+  a.ldx = x_kdim;
+  a.x_div = 1;
+  a.p[0] = Proj{w, nullptr};
+  a.kind = kBf16KBlocked;
+  a.E = 1;
+  a.N = (int)result_n;
+  a.K = (int)x_kdim;
+  a.gsize = kChunk;
+  a.nchunks = (int)((x_kdim + kChunk - 1) / kChunk);
+  a.vec = aligned16(w);
+  a.batch = batch_for(a.nchunks);
+  a.rows = Rows{nullptr, nullptr, nullptr, nullptr, (int)x_m};
+  const hipError_t e = launch_norm_dense(a, residual, x_out, gamma, eps, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
+}
+
 int uocr_rms_norm(float* out, float* x_out, const float* x, const float* residual, const float* gamma, int64_t rows,
                   int64_t dim, float eps, void* stream, char* err, size_t errlen) {
   const char* op = "rms_norm";

@@ -25,6 +25,7 @@ from .ops import (
     paged_decode_attention_qkv,
     quantize_per_group,
     rms_norm,
+    rms_norm_dense_bf16_qmv,
     rope,
     swiglu,
 )
@@ -54,6 +55,7 @@ __all__ = [
     "paged_decode_attention_qkv",
     "quantize_per_group",
     "rms_norm",
+    "rms_norm_dense_bf16_qmv",
     "rope",
     "rope_tables",
     "swiglu",

@@ -52,6 +52,8 @@ SIGNATURES: dict[str, list] = {
     "uocr_paged_decode_attention_qkv": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64,
                                         _i64, _i64, _vp, _i64, _vp, _i64, _vp, ctypes.c_float, _vp, _sz, _vp, _cp,
                                         _sz],
+    "uocr_rms_norm_dense_bf16_qmv": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_float, _vp, _i64, _i64,
+                                     _i64, _vp, _cp, _sz],
     "uocr_rms_norm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _cp, _sz],
     "uocr_rope": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _cp, _sz],
     "uocr_swiglu": [_vp, _vp, _i64, _i64, _vp, _cp, _sz],

@@ -3,7 +3,8 @@
 
 Per layer, for ``B`` rows (one token of each of ``B`` requests):
 
-* ``input_layernorm`` (with the previous layer's residual add fused in: :func:`ops.rms_norm`);
+* ``input_layernorm`` (with the previous layer's residual add fused in: :func:`ops.rms_norm`, or, at
+  one or two rows, inside the q/k/v projection: :func:`ops.rms_norm_dense_bf16_qmv`);
 * one ``dense_bf16_qmv`` over the q, k and v projections at once (their K-blocked weights side by side
   along N, the reference's three ``Projection.decode_rows`` calls in one launch);
 * :func:`ops.paged_decode_attention_qkv`: RoPE of q and k at each row's position and the paged attention
@@ -89,21 +90,31 @@ class DecoderLayer:
             self.down = weights[m + "down_proj.weight"].contiguous()
 
     def decode(self, x: torch.Tensor, delta: torch.Tensor | None, *, positions: torch.Tensor, cos: torch.Tensor,
-               sin: torch.Tensor, kv: ops.PagedKv, scale: float, moe_workspace: torch.Tensor | None = None,
-               attn_workspace: torch.Tensor | None = None) -> torch.Tensor:
-        """``x [B, hidden]`` is the residual stream; ``delta`` the previous layer's output, added to ``x``
-        in place before this layer's input norm.  Returns this layer's output (the next ``delta``)."""
+               sin: torch.Tensor, kv: ops.PagedKv, scale: float, spare: torch.Tensor | None = None,
+               moe_workspace: torch.Tensor | None = None,
+               attn_workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """``x [B, hidden]`` is the residual stream; ``delta`` the previous layer's output, added to it before
+        this layer's input norm.  Returns ``(this layer's output, the buffer that now holds the stream)``.
+
+        Without ``spare`` the add is in place (``x``) and the norm a launch of its own; with ``spare`` (rows
+        <= :data:`ops.NORM_DENSE_MAX_ROWS`) the norm runs inside the q/k/v projection and the sum lands in
+        ``spare`` -- the same bits either way."""
         c = self.config
         rows, heads = x.shape[0], c.num_attention_heads
-        normed = ops.rms_norm(x, self.input_norm, c.rms_norm_eps, residual=delta)
-        qkv = ops.dense_bf16_qmv(normed, self.qkv)
+        if spare is not None:
+            qkv = ops.rms_norm_dense_bf16_qmv(x, self.input_norm, c.rms_norm_eps, self.qkv, residual=delta,
+                                              x_out=None if delta is None else spare)
+            x = x if delta is None else spare
+        else:
+            normed = ops.rms_norm(x, self.input_norm, c.rms_norm_eps, residual=delta)
+            qkv = ops.dense_bf16_qmv(normed, self.qkv)
         attended = ops.paged_decode_attention_qkv(qkv, positions, cos, sin, heads=heads, kv=kv,
                                                   layer_idx=self.layer_idx, scale=scale, workspace=attn_workspace)
         attn_out = ops.dense_bf16_qmv(attended.view(rows, c.hidden_size), self.o_proj)
         normed = ops.rms_norm(x, self.post_norm, c.rms_norm_eps, residual=attn_out)
         if self.moe is not None:
-            return self.moe.decode_rows(normed, workspace=moe_workspace)
-        return ops.dense_bf16_qmv(ops.swiglu(ops.dense_bf16_qmv(normed, self.gate_up)), self.down)
+            return self.moe.decode_rows(normed, workspace=moe_workspace), x
+        return ops.dense_bf16_qmv(ops.swiglu(ops.dense_bf16_qmv(normed, self.gate_up)), self.down), x
 
 
 class Decoder:
@@ -122,16 +133,23 @@ class Decoder:
         self.scale = 1.0 / float(np.sqrt(config.head_dim))
 
     def decode(self, hidden: torch.Tensor, *, positions: torch.Tensor, kv: ops.PagedKv,
-               moe_workspace: torch.Tensor | None = None,
-               attn_workspace: torch.Tensor | None = None) -> torch.Tensor:
-        """One token for each of ``B`` requests: ``hidden [B, hidden]`` (updated in place as the residual
-        stream), ``positions`` int32 ``[B]``; every layer stores its new k/v rows through ``kv``.  Returns
-        the final norm of the last hidden state, ``[B, hidden]``."""
-        delta = None
+               moe_workspace: torch.Tensor | None = None, attn_workspace: torch.Tensor | None = None,
+               scratch: torch.Tensor | None = None, fuse_norm: bool = True) -> torch.Tensor:
+        """One token for each of ``B`` requests: ``hidden [B, hidden]`` (used, with ``scratch`` of the same
+        shape, to hold the residual stream: its contents afterwards are unspecified), ``positions`` int32
+        ``[B]``; every layer stores its new k/v rows through ``kv``.  Returns the final norm of the last
+        hidden state, ``[B, hidden]``.  At ``B <=`` :data:`ops.NORM_DENSE_MAX_ROWS` the input norms run
+        inside the q/k/v projections (``fuse_norm=False`` keeps them apart; the bits are the same)."""
+        fused = fuse_norm and hidden.shape[0] <= ops.NORM_DENSE_MAX_ROWS
+        if fused and scratch is None:
+            scratch = torch.empty_like(hidden)
+        cur, delta = hidden, None
         for layer in self.layers:
-            delta = layer.decode(hidden, delta, positions=positions, cos=self.cos, sin=self.sin, kv=kv,
-                                 scale=self.scale, moe_workspace=moe_workspace, attn_workspace=attn_workspace)
-        return ops.rms_norm(hidden, self.norm, self.config.rms_norm_eps, residual=delta)
+            spare = (scratch if cur is hidden else hidden) if fused else None
+            delta, cur = layer.decode(cur, delta, positions=positions, cos=self.cos, sin=self.sin, kv=kv,
+                                      scale=self.scale, spare=spare, moe_workspace=moe_workspace,
+                                      attn_workspace=attn_workspace)
+        return ops.rms_norm(cur, self.norm, self.config.rms_norm_eps, residual=delta)
 
     def logits_rows(self, normed: torch.Tensor) -> torch.Tensor:
         """``lm_head`` over every row, fp32 ``[B, vocab]`` (decoder.py:802-804)."""

@@ -218,6 +218,34 @@ def _rows_view(op: str, name: str, t, like=None) -> torch.Tensor:
     return t
 
 
+#: The fused norm + projection takes at most this many rows (and K <= 2048, N < 16384).
+NORM_DENSE_MAX_ROWS = 2
+
+
+def rms_norm_dense_bf16_qmv(x, gamma, eps: float, w, *, residual=None, x_out=None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """:func:`rms_norm` then :func:`dense_bf16_qmv` in one launch, with their bits, for decode rows
+    (at most :data:`NORM_DENSE_MAX_ROWS`): ``rmsnorm(x + residual) * gamma @ W^T``.  With ``residual``,
+    ``x + residual`` is written to ``x_out``, which must be another buffer than ``x`` and ``residual``."""
+    op = "rms_norm_dense_bf16_qmv"
+    x = _gpu(op, "x", x, torch.float32, 2)
+    gamma = _gpu(op, "gamma", gamma, torch.float32, 1)
+    w = _gpu(op, "w", w, torch.bfloat16, 3)
+    if residual is not None:
+        residual = _gpu(op, "residual", residual, torch.float32, 2)
+        if x_out is None:
+            raise ValueError(f"{op}: a residual add needs x_out")
+        if residual.shape != x.shape or tuple(x_out.shape) != tuple(x.shape) or not x_out.is_contiguous():
+            raise ValueError(f"{op}: residual and x_out must be contiguous {tuple(x.shape)} tensors")
+    if out is None:
+        out = torch.empty((x.shape[0], w.shape[1]), device=x.device, dtype=torch.float32)
+    out = _gpu(op, "result", out, torch.float32, 2)
+    _lib.call("uocr_rms_norm_dense_bf16_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0],
+              x.shape[1], _ptr(residual), _ptr(x_out), gamma.data_ptr(), float(eps), w.data_ptr(), w.shape[0],
+              w.shape[1], w.shape[2], _stream(x))
+    return out
+
+
 def rope(q, k, positions, cos_table, sin_table, *, v=None, q_out=None, k_out=None, v_out=None):
     """``Attention._rope`` on the decode rows (decoder.py:459-462,487-491) with the cos / sin rows gathered
     at ``positions`` (``rope_rows``, decoder.py:766-775): ``q``, ``k`` ``[rows, heads, head_dim]`` (``k``
