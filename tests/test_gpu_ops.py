@@ -248,7 +248,9 @@ def _rand_dense(oracle, seed, m, n_, k):
 
 
 @pytest.mark.parametrize(("m", "n_", "k"), [(1, 24, 64), (5, 24, 64), (8, 40, 96), (13, 7, 32), (9, 1792, 1280),
-                                            (3, 1280, 1792), (2, 3840, 1280), (1, 129, 6848), (2, 1280, 6848)])
+                                            (3, 1280, 1792), (2, 3840, 1280), (1, 129, 6848), (2, 1280, 6848),
+                                            (8, 1280, 1280), (4, 3840, 1280), (6, 1280, 6848), (7, 13696, 1280),
+                                            (5, 100, 1008)])
 def test_dense_every_tile(ops, oracle, m, n_, k) -> None:
     x, w = _rand_dense(oracle, m * 1000 + n_ + k, m, n_, k)
     want = oracle.dense_bf16_qmv_chunked(x, w)
@@ -258,6 +260,32 @@ def test_dense_every_tile(ops, oracle, m, n_, k) -> None:
         assert bits_equal(got, want), tile
         assert bits_equal(got, alone), tile
     assert oracle.rel_err(want, oracle.dense_f64(x, w)) <= 1e-5
+
+
+def test_dense_eight_rows_in_graph_replays(ops, oracle) -> None:
+    """8 rows of a 1280-wide projection, captured three times in a graph: replays, with eager calls between
+    them, give the eager bits every time."""
+    x, w = _rand_dense(oracle, 77, 8, 1280, 1280)
+    xg, wg = t(x), t(w)
+    eager = n(ops.dense_bf16_qmv(xg, wg))
+    assert bits_equal(eager, oracle.dense_bf16_qmv_chunked(x, w))
+    out = torch.empty((8, 1280), device="cuda:0")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.dense_bf16_qmv(xg, wg, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(3):
+            ops.dense_bf16_qmv(xg, wg, out=out)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bits_equal(n(out), eager)
+        assert bits_equal(n(ops.dense_bf16_qmv(xg, wg)), eager)
 
 
 def test_dense_one_hot_zero_and_empty(ops, oracle) -> None:
