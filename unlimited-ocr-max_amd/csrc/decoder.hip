@@ -28,7 +28,11 @@ constexpr int kNormThreads = 256;
 
 // One workgroup per row.  Sum of squares: thread t chains fma(v, v, s) over
 // elements t, t + 256, ...; the 64 lanes of a wave add by a halving tree; the
-// 4 wave sums add as (w0 + w1) + (w2 + w3).
+// 4 wave sums add as (w0 + w1) + (w2 + w3).  A thread keeps its elements (and
+// their gamma) in registers between the two passes when the row has at most
+// kNormRegs * 256 of them, so the second pass reads nothing from memory.
+constexpr int kNormRegs = 8;
+
 template <bool RESID>
 __global__ void __launch_bounds__(kNormThreads) k_add_rmsnorm(float* __restrict__ out, float* x_out, const float* x,
                                                               const float* __restrict__ delta,
@@ -39,14 +43,38 @@ __global__ void __launch_bounds__(kNormThreads) k_add_rmsnorm(float* __restrict_
   const float* dr = RESID ? delta + row * dim : nullptr;
   float* xo = RESID ? x_out + row * dim : nullptr;
   const int tid = (int)threadIdx.x;
+  const bool regs = dim <= kNormRegs * kNormThreads;
+  float vk[kNormRegs], gk[kNormRegs];
   float ss = 0.0f;
-  for (int i = tid; i < dim; i += kNormThreads) {
-    float v = xr[i];
-    if constexpr (RESID) {
-      v = v + dr[i];
-      xo[i] = v;  // x_out may be x: each element is read then written by the same thread
+  if (regs) {
+#pragma unroll
+    for (int j = 0; j < kNormRegs; ++j) {
+      const int i = tid + j * kNormThreads;
+      vk[j] = 0.0f;
+      gk[j] = 0.0f;
+      if (i < dim) {
+        vk[j] = xr[i];
+        if constexpr (RESID) vk[j] = vk[j] + dr[i];
+        gk[j] = ldg(gamma + i);
+      }
     }
-    ss = __builtin_fmaf(v, v, ss);
+#pragma unroll
+    for (int j = 0; j < kNormRegs; ++j) {
+      const int i = tid + j * kNormThreads;
+      if (i < dim) {
+        if constexpr (RESID) xo[i] = vk[j];  // x_out may be x: each element is read then written by the same thread
+        ss = __builtin_fmaf(vk[j], vk[j], ss);
+      }
+    }
+  } else {
+    for (int i = tid; i < dim; i += kNormThreads) {
+      float v = xr[i];
+      if constexpr (RESID) {
+        v = v + dr[i];
+        xo[i] = v;
+      }
+      ss = __builtin_fmaf(v, v, ss);
+    }
   }
   ss = tree_sum(ss);
   if (lane_id() == 0) red[tid / kWave] = ss;
@@ -54,10 +82,18 @@ __global__ void __launch_bounds__(kNormThreads) k_add_rmsnorm(float* __restrict_
   ss = (red[0] + red[1]) + (red[2] + red[3]);
   const float r = 1.0f / sqrtf(ss / (float)dim + eps);
   float* yr = out + row * dim;
-  for (int i = tid; i < dim; i += kNormThreads) {
-    float v = xr[i];
-    if constexpr (RESID) v = xo[i];
-    yr[i] = (v * r) * ldg(gamma + i);
+  if (regs) {
+#pragma unroll
+    for (int j = 0; j < kNormRegs; ++j) {
+      const int i = tid + j * kNormThreads;
+      if (i < dim) yr[i] = (vk[j] * r) * gk[j];
+    }
+  } else {
+    for (int i = tid; i < dim; i += kNormThreads) {
+      float v = xr[i];
+      if constexpr (RESID) v = xo[i];
+      yr[i] = (v * r) * ldg(gamma + i);
+    }
   }
 }
 
