@@ -245,6 +245,38 @@ def test_prefill_rows_do_not_depend_on_the_batch(oracle, full_int8) -> None:
     assert bits_equal(whole[:40], part)
 
 
+@pytest.mark.parametrize("T", [512, 2048])
+def test_prefill_graph_replays(oracle, full_int8, T) -> None:
+    """The prefill's routing counters are cleared inside its own launches (no memset in a graph): the layer
+    captured in a HIP graph, replayed several times with another eager prefill between the replays, gives
+    the eager bits every time.  T = 512 takes the one-launch routing, T = 2048 the many-workgroup counts."""
+    moe = moe_for(full_int8)
+    rng = np.random.default_rng(T)
+    x = oracle.rmsnorm_rows(rng, T, 1280)
+    x2 = oracle.rmsnorm_rows(rng, T // 2, 1280)
+    ws = moe.workspace(T, prefill=True)
+    xg = t(x)
+    want = n(moe(xg, workspace=ws))
+    want2 = n(moe(t(x2)))
+    assert bits_equal(n(moe(xg, workspace=ws)), want)  # deterministic back to back
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe(xg, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outg = moe(xg, workspace=ws)
+    for _ in range(3):
+        outg.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bits_equal(n(outg), want)
+        assert bits_equal(n(moe(t(x2))), want2)
+
+
 def test_unaligned_output_pointer(oracle, small) -> None:
     """The C entry points accept an out pointer that is only 4-byte aligned (the combine's one-column path):
     same bits as an aligned buffer, for the prefill and the multi-kernel decode (B = 40)."""
