@@ -30,11 +30,14 @@ namespace uocr {
 namespace {
 
 constexpr int kD = 128;          // head dim
-constexpr int kThreads = 256;    // 4 waves
+// 8 waves: half a split's loads per thread (100 VGPRs, 4 waves a SIMD) ran
+// faster than 4 waves holding all of them (170 VGPRs)
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
 constexpr int kLanesPerRow = 8;  // 16 floats of q.k per lane: float4 sub, sub + 8, sub + 16, sub + 24
-constexpr int kRowsPerPass = kThreads / kLanesPerRow;  // 32 rows scored at once by the workgroup
+constexpr int kRowsPerPass = kThreads / kLanesPerRow;  // 64 rows scored at once by the workgroup
 constexpr int kPart = kD + 4;  // floats per partial: the value sum, max, sum of exp, 2 pad (16-byte records)
-constexpr int kValueGroups = kThreads / (kD / 4);      // 8 value rows at once, a float4 column per lane
+constexpr int kValueGroups = kThreads / (kD / 4);      // 16 value rows at once, a float4 column per lane
 constexpr int kKRows = kAttnSplitRows / kRowsPerPass;   // k rows per lane group
 constexpr int kVRows = kAttnSplitRows / kValueGroups;   // v rows per lane
 
@@ -218,7 +221,9 @@ __device__ __forceinline__ void split_partial(const PagedArgs& a, const float* _
   m = tree_max(m);
   if (lane_id() == 0) red[tid / 64] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  m = red[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) m = fmaxf(m, red[i]);
   __syncthreads();
   float l = 0.0f;
   for (int i = tid; i < n; i += kThreads) {
@@ -229,7 +234,8 @@ __device__ __forceinline__ void split_partial(const PagedArgs& a, const float* _
   l = tree_sum(l);
   if (lane_id() == 0) red[tid / 64] = l;
   __syncthreads();
-  l = (red[0] + red[1]) + (red[2] + red[3]);
+  static_assert(kWaves == 8, "the sum below adds 8 wave sums");
+  l = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
   // ---- value sums: thread (g, c): rows i = g mod 8, float4 column c; the 8 groups added at the end
   f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
