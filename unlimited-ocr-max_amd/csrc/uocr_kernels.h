@@ -70,7 +70,7 @@ constexpr int kGemvMaxThreads = kGemvMaxWaves * 64;
 constexpr int kGemvMaxBatch = 16;
 
 // dense_bf16_qmv: below kDenseNarrowMaxN output columns and for at most
-// kDenseNarrowMaxRows rows, a (column, chunk) lane mapping (16 columns a
+// kDenseNarrowMaxRows rows, a (column, chunk) lane mapping (8 columns a
 // workgroup, the same bits); else launch_gemv.
 constexpr int kDenseNarrowMaxN = 16384;
 constexpr int kDenseNarrowMaxRows = 2;
