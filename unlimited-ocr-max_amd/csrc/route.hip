@@ -142,13 +142,22 @@ __device__ __forceinline__ void logits_tile(float* __restrict__ logits, uint16_t
       }
     }
   }
+  // the trees of all TW x EW values at once: lane 16 r of sums[j] holds
+  // value 4 j + tree_row_value(r) of p (row-major), one store per 4 values
+  static_assert(EW % 4 == 0, "a quad of values shares its token");
+  float flat[TW * EW], sums[TW * EW / 4];
 #pragma unroll
   for (int t = 0; t < TW; ++t)
 #pragma unroll
-    for (int e = 0; e < EW; ++e) {
-      const float v = tree_sum(p[t][e]);
-      if (l == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = v;
-    }
+    for (int e = 0; e < EW; ++e) flat[t * EW + e] = p[t][e];
+  tree_sum_quads(flat, sums);
+  const int e_row = tree_row_value(l >> 4);
+#pragma unroll
+  for (int j = 0; j < TW * EW / 4; ++j) {
+    const int t = 4 * j / EW;
+    const int e = 4 * j % EW + e_row;
+    if ((l & 15) == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = sums[j];
+  }
 }
 
 template <int TW, int EW>

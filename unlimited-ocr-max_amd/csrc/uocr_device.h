@@ -195,6 +195,35 @@ __device__ __forceinline__ float tree_sum(float v) {
   v = v + from_up<1>(v);
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
+// tree_sum of N values at once, with the same additions in the same order.
+// The two steps across 16-lane rows run on pairs of values:
+// permlane32_swap(a, b) leaves [a lo, b lo] and [a hi, b hi], whose sum holds
+// a's step-32 partials in lanes 0-31 and b's in lanes 32-63; permlane16_swap
+// does the same for rows.  Lane 16 r of out[j] then holds the total of
+// v[4 j + tree_row_value(r)] (rows hold values 0, 2, 1, 3 of the quad).
+__device__ __forceinline__ int tree_row_value(int r) { return ((r & 1) << 1) | (r >> 1); }
+template <int N>
+__device__ __forceinline__ void tree_sum_quads(const float (&v)[N], float (&out)[N / 4]) {
+  static_assert(N % 4 == 0, "values come in quads");
+  float c[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * i]), __float_as_uint(v[2 * i + 1]),
+                                                    false, false);
+    c[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int j = 0; j < N / 4; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(c[2 * j]), __float_as_uint(c[2 * j + 1]),
+                                                    false, false);
+    float e = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    e = e + from_up<8>(e);
+    e = e + from_up<4>(e);
+    e = e + from_up<2>(e);
+    e = e + from_up<1>(e);
+    out[j] = e;
+  }
+}
 __device__ __forceinline__ float tree_max(float v) {
   v = fmaxf(v, from_up<32>(v));
   v = fmaxf(v, from_up<16>(v));
