@@ -21,9 +21,10 @@ namespace {
 // logits[t][e] for 4 tokens x 4 experts per wave (grid: 16 experts per
 // workgroup in x, 4 tokens in y), H <= kLogitsMaxH: the lane's x and router
 // values (k = lane + 64 j) are all loaded before the fmas, then each (t, e)
-// is the 64-lane tree (DPP, the order of wave_tree_sum).  The waves of the
-// first expert group also write the tokens' x rows rounded to bf16 (xb),
-// when asked: the prefill GEMM's A operand.
+// is the 64-lane tree (the order of wave_tree_sum, batched by
+// tree_sum_quads).  The waves of the first expert group also write the
+// tokens' x rows rounded to bf16 (xb), when asked: the prefill GEMM's A
+// operand.
 constexpr int kLogitsMaxH = 2048;
 
 // The first workgroup of a launch clears `n` words for a later kernel of the
@@ -69,18 +70,24 @@ __global__ void __launch_bounds__(256) k_logits_wide(float* __restrict__ logits,
       }
     }
   }
+  float p[16], sums[4];  // p[4 ti + ei]
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
 #pragma unroll
     for (int ei = 0; ei < 4; ++ei) {
-      float p = 0.0f;
+      float a = 0.0f;
 #pragma unroll
       for (int j = 0; j < kJ; ++j)
-        if (j < nj) p = __builtin_fmaf(xv[ti][j], wv[ei][j], p);
-      const float v = tree_sum(p);
-      if (l == 0 && t0 + ti < T && e0 + ei < E) logits[(int64_t)(t0 + ti) * E + e0 + ei] = v;
+        if (j < nj) a = __builtin_fmaf(xv[ti][j], wv[ei][j], a);
+      p[4 * ti + ei] = a;
     }
   }
+  // lane 16 r of sums[ti] holds token ti's logit of expert e0 + tree_row_value(r)
+  tree_sum_quads(p, sums);
+  const int ei = tree_row_value(l >> 4);
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+    if ((l & 15) == 0 && t0 + ti < T && e0 + ei < E) logits[(int64_t)(t0 + ti) * E + e0 + ei] = sums[ti];
 }
 
 // logits[t][e] for TW tokens x EW experts per wave (grid: x = blocks of EW
