@@ -56,6 +56,21 @@ def test_gate_bitwise(oracle, T) -> None:
     assert bits_equal(n(wts), wts_o)
 
 
+@pytest.mark.parametrize(("T", "H", "E"), [(3, 100, 64), (20, 100, 40), (5, 2112, 64), (20, 2112, 40)])
+def test_gate_general_widths(oracle, T, H, E) -> None:
+    """H that is not a multiple of 64, or above 2048, takes the general logits kernel (lanes past H add +0;
+    4 tokens x 1 expert or 16 x 4 per wave); E = 40 leaves part of the last expert block empty."""
+    from uocr_moe import gate
+
+    rng = np.random.default_rng(T * 7 + H)
+    x = oracle.rmsnorm_rows(rng, T, H)
+    router = rng.standard_normal((E, H), dtype=np.float32) * np.float32(0.05)
+    idx, wts = gate(t(x), t(router), 6)
+    ids_o, wts_o = oracle.moe_gate(x, router, 6)
+    assert np.array_equal(n(idx), ids_o.astype(np.int64))
+    assert bits_equal(n(wts), wts_o)
+
+
 def test_gate_ties_and_renorm(oracle) -> None:
     from uocr_moe import gate
 

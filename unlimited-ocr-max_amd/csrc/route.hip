@@ -219,13 +219,21 @@ __global__ void __launch_bounds__(256) k_logits(float* __restrict__ logits, cons
         for (int e = 0; e < EE; ++e) p[t][e] = __builtin_fmaf(xv[u][t], wv[u][e], p[t][e]);
     }
   }
+  // lane 16 r of sums[j] holds value 4 j + tree_row_value(r) of p (row-major)
+  static_assert(TT * EE % 4 == 0, "values come in quads");
+  float flat[TT * EE], sums[TT * EE / 4];
 #pragma unroll
   for (int t = 0; t < TT; ++t)
 #pragma unroll
-    for (int e = 0; e < EE; ++e) {
-      const float v = wave_tree_sum(p[t][e]);
-      if (lane == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = v;
-    }
+    for (int e = 0; e < EE; ++e) flat[t * EE + e] = p[t][e];
+  tree_sum_quads(flat, sums);
+  const int rv = tree_row_value(lane >> 4);
+#pragma unroll
+  for (int j = 0; j < TT * EE / 4; ++j) {
+    const int t = (4 * j + rv) / EE;
+    const int e = (4 * j + rv) % EE;
+    if ((lane & 15) == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = sums[j];
+  }
 }
 
 // ---------------------------------------------------------------- softmax + top-k
