@@ -16,7 +16,8 @@
  * the grouping tables and the layer intermediates comes from the `workspace`
  * argument when one is given (size: uocr_moe_workspace_bytes), else from a
  * buffer the library keeps per device and stream (grown on demand, so a call
- * under stream capture passes its own workspace).
+ * under stream capture passes its own workspace).  A superseded library
+ * buffer is kept until uocr_moe_release, so graphs captured with it stay valid.
  */
 #ifndef UOCR_MOE_H
 #define UOCR_MOE_H
@@ -75,6 +76,18 @@ int uocr_int8_dequant_expert(void* result, int64_t result_n, int64_t result_kdim
                              const float* scales, int64_t s_e, int64_t s_n, int64_t s_groups,
                              const int32_t* expert_idx, int64_t idx_len,
                              void* stream, char* err, size_t errlen);
+
+/* quantize_per_group -- replaces quantize_per_group (tools/quantize_int8.py:298-329;
+ * the format of tools/quantize_int8.py:54-70), on the device.
+ *   w fp32 (w_bf16 = 0) or bf16 bits (w_bf16 = 1) [rows, K] -> q int8 [rows, K],
+ *   scales fp32 [rows, K/group]: per group of `group` elements along K,
+ *   amax = max |w|, scale = amax / 127 (1.0 when amax == 0),
+ *   q = clip(rint(w / scale), -127, 127), fp32 divisions correctly rounded and
+ *   rint half to even (bitwise the reference's numpy arithmetic).  NaN or Inf
+ *   in w is not detected here (the Python wrapper refuses it, as the
+ *   reference's tool does). */
+int uocr_quantize_per_group(int8_t* q, float* scales, const void* w, int w_bf16, int64_t rows, int64_t kdim,
+                            int64_t group, void* stream, char* err, size_t errlen);
 
 /* ngram_block -- replaces NgramBlock.execute
  * (unlimited_ocr_max/kernels/ngram_block.mojo:60-151; staged by apply_ngram_guard,
@@ -265,9 +278,14 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden,
  * control words.  No call may be in flight. */
 void uocr_moe_release(void);
 
-/* Waits for `stream` and reports whether any persistent decode launch on it
- * ran out of its bounded waits (errors = 1: those launches' outputs are wrong).
- * No counterpart in the reference; a diagnostic of this build's decode kernel. */
+/* Waits for `stream` and reports whether a persistent decode launch on it ran
+ * out of its bounded waits: errors = 1.
+ * Such a launch wrote NaN where its outputs depended on what it waited for,
+ * and every later launch on the same slot writes NaN until this call, which
+ * then clears the slot (control words and tagged arena).  The waits run out
+ * only when the persistent kernel's workgroups cannot all be resident, i.e.
+ * another kernel holds CUs for tens of milliseconds.  No counterpart in the
+ * reference; the error path of this build's decode kernel. */
 int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen);
 
 /* Arms a phase trace for the next persistent decode launch: for task i it

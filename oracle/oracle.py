@@ -433,6 +433,26 @@ def moe_layer_f64(x, layer: MoeWeights, ids=None, wts=None, bf16_dequant: bool =
     return out
 
 
+def moe_layer_f64_grouped(x, layer: MoeWeights, ids, wts, bf16_dequant: bool = False,
+                          rows: np.ndarray | None = None) -> np.ndarray:
+    """:func:`moe_layer_f64` with each expert's tokens batched into one float64 matmul (same closed form,
+    other summation order; for prefill-sized T).  ``rows`` restricts the result to those token rows."""
+    xf = np.asarray(x, np.float64)
+    ids = np.asarray(ids)
+    wts = np.asarray(wts, np.float64)
+    if rows is not None:
+        xf, ids, wts = xf[rows], ids[rows], wts[rows]
+    gate, up, down = routed_stacks_f64(layer, bf16_dequant)
+    sg, su, sd = (bf16_values(unkblocked(w)).astype(np.float64) for w in (layer.sh_gate, layer.sh_up, layer.sh_down))
+    out = (_silu64(xf @ sg.T) * (xf @ su.T)) @ sd.T
+    for e in np.unique(ids):
+        tok, slot = np.nonzero(ids == e)
+        xe = xf[tok]
+        y = (_silu64(xe @ gate[e].T) * (xe @ up[e].T)) @ down[e].T
+        np.add.at(out, tok, wts[tok, slot][:, None] * y)
+    return out
+
+
 # ---------------------------------------------------------------------------
 # the n-gram guard (unlimited_ocr_max/kernels/ngram_block.mojo)
 # ---------------------------------------------------------------------------

@@ -10,8 +10,11 @@
   max relative error 1e-2 of the float64 layer on the reference's prefill
   weights, ``bf16_rne(f32(q) * scale)`` (the int8 path's int8_dequant_expert values;
   decoder.py:568-584) -- the north-star tolerance for the bf16-MFMA layer.
-  Shapes: the served layer (64 experts, 1280/896, 2 shared) at T = 64 and 512,
-  with Zipf-skewed and adversarial (all tokens on experts 0-5) routing.
+  Shapes: the served layer (64 experts, 1280/896, 2 shared) at T = 64, 512 and
+  2048 on RMS-normalised rows (near-uniform routing), and T = 512 with the
+  adversarial routing (all tokens on experts 0-5).  The benchmark's skewed
+  workloads (Zipf routing at T = 512 and 4096, the T = 4096 adversarial case)
+  and the chained 11-layer decode are in test_gpu_configs.py.
 """
 
 from __future__ import annotations
@@ -310,3 +313,47 @@ def test_unaligned_output_pointer(oracle, small) -> None:
         _lib.call(entry, buf.data_ptr() + 4, x.data_ptr(), T, H, ctypes.byref(moe._layer), None, None, ws.data_ptr(),
                   ws.numel(), _stream(x))
         assert bits_equal(n(buf[1:].view(T, H)), n(ref)), entry
+
+
+def test_decode_failure_is_loud_and_recoverable(oracle, small, monkeypatch) -> None:
+    """The persistent kernel's bounded waits, forced to run out from the host (a spin limit of one poll),
+    end the launch normally with NaN outputs and the error word set; later launches on the slot write NaN
+    until ``fused_errors`` reports and clears it; the next launch is bitwise the oracle again."""
+    from uocr_moe import _lib
+
+    layer = small[True]
+    moe = moe_for(layer)
+    x = np.random.default_rng(31).standard_normal((4, 256)).astype(np.float32)
+    want = oracle.moe_decode_exact(x, layer)[0]
+    assert bits_equal(n(moe.decode_rows(t(x))), want)
+    assert _lib.fused_errors() == 0
+    monkeypatch.setenv("UOCR_MOE_SPIN_LIMIT", "1")
+    failed = n(moe.decode_rows(t(x)))
+    monkeypatch.delenv("UOCR_MOE_SPIN_LIMIT")
+    assert np.isnan(failed).any()
+    assert np.isnan(n(moe.decode_rows(t(x)))).all()  # the slot stays poisoned
+    assert _lib.fused_errors() == 1  # reported, and cleared
+    assert bits_equal(n(moe.decode_rows(t(x))), want)
+    assert _lib.fused_errors() == 0
+
+
+def test_decode_on_many_streams(oracle, small) -> None:
+    """Each stream owns its control slot (no sharing past a first chunk of slots); eager persistent launches
+    on different streams are ordered, so each keeps the whole device: all bitwise the oracle."""
+    from uocr_moe import _lib
+
+    layer = small[True]
+    moe = moe_for(layer)
+    xs = [np.random.default_rng(400 + i).standard_normal((1 + i % 8, 256)).astype(np.float32) for i in range(10)]
+    want = [oracle.moe_decode_exact(x, layer)[0] for x in xs]
+    streams = [torch.cuda.Stream() for _ in range(10)]
+    outs = []
+    for rep in range(2):
+        for s, x in zip(streams, xs):
+            with torch.cuda.stream(s):
+                outs.append(moe.decode_rows(t(x)))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert bits_equal(n(o), want[i % 10]), i
+    for s in streams:
+        assert _lib.fused_errors(s.cuda_stream) == 0

@@ -177,3 +177,11 @@ def test_layer_refusals() -> None:
     layer = _lib.Layer(64, 1280, 896, 1792, 6, 128, 1, 0)
     msg = _err("uocr_moe_forward", None, None, 1, 1024, ctypes.byref(layer), None, None, None, 0, None)
     assert msg == "uocr_moe_forward: x and the layer disagree on hidden"
+
+
+def test_quantize_refusals() -> None:
+    """tools/quantize_int8.py:306-308: a partial trailing group is refused, not quantised."""
+    assert _err("uocr_quantize_per_group", 8, 8, 8, 0, 2, 100, 128, None) == \
+        "quantize_per_group: K=100 is not divisible by the group size 128"
+    assert "bad group size" in _err("uocr_quantize_per_group", 8, 8, 8, 0, 2, 128, 0, None)
+

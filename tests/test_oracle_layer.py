@@ -73,3 +73,22 @@ def test_a_wrong_expert_breaks_the_float64_match(oracle, small_layers) -> None:
     bad = ids.copy()
     bad[0, 0], bad[0, 5] = ids[0, 5], ids[0, 0]
     assert oracle.rel_err(out, oracle.moe_layer_f64(x, layer, bad, wts)) > 1e-3
+
+
+@pytest.mark.parametrize("int8", [True, False], ids=["int8", "bf16"])
+def test_grouped_float64_layer_equals_the_per_token_form(oracle, small_layers, int8: bool) -> None:
+    """The expert-batched float64 layer (used at prefill sizes) is the per-token closed form up to float64
+    rounding, with either dequantisation, and on a row subset; a planted wrong routing weight breaks it."""
+    layer = small_layers[int8]
+    x = np.random.default_rng(26).standard_normal((40, 256)).astype(np.float32)
+    ids, wts = oracle.moe_gate(x, layer.router, 6)
+    for bf in (False, True):
+        per_token = oracle.moe_layer_f64(x, layer, ids, wts, bf16_dequant=bf)
+        grouped = oracle.moe_layer_f64_grouped(x, layer, ids, wts, bf16_dequant=bf)
+        assert oracle.rel_err(grouped, per_token) <= 1e-12
+        rows = np.array([3, 0, 39, 17])
+        sub = oracle.moe_layer_f64_grouped(x, layer, ids, wts, bf16_dequant=bf, rows=rows)
+        assert oracle.rel_err(sub, per_token[rows]) <= 1e-12
+    bad = wts.copy()
+    bad[5, 2] *= 1.5
+    assert oracle.rel_err(oracle.moe_layer_f64_grouped(x, layer, ids, bad), oracle.moe_layer_f64(x, layer, ids, wts)) > 1e-4

@@ -38,8 +38,12 @@
 // carry the tag of the current launch: no counters and no fences on the data
 // path.  Each workgroup computes the routing itself from the tagged logits.
 // A task waits only on tasks with smaller indices and every workgroup of the
-// grid is resident (the grid is sized to the occupancy), so the waits end;
-// each wait is also bounded and records an error if it ever runs out.  The
+// grid is resident (the grid is sized to the occupancy), so the waits end.
+// Each wait is also bounded: one that runs out (another kernel holding CUs
+// for tens of milliseconds) sets the error word and takes NaN for what it
+// waited for, so the launch still ends with NaN in the outputs that depend on
+// it; while the word stays set, every later launch on the slot writes NaN,
+// until the host reads and clears it (uocr_moe_fused_errors).  The
 // launch tag is the control word EPOCH + 1: every wave reads EPOCH at its
 // start, each workgroup then adds one to ARRIVED (a non-returning atomic),
 // and the last of the comb tasks (the only counter, H/64 x B increments) waits
@@ -56,7 +60,6 @@ namespace {
 constexpr int kWaves = kFusedWaves;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kXPad = kFusedXPad;
-constexpr uint32_t kSpinLimit = 1u << 16;  // polls per wait (tens of ms): real waits take microseconds
 
 // control words
 constexpr int C_EPOCH = 0, C_ARRIVED = 1, C_COMBINED = 2, C_ERR = 4;
@@ -107,21 +110,25 @@ __device__ __forceinline__ void st_pair(uint64_t* p, float v, uint32_t tag) {
 __device__ __forceinline__ float pair_value(uint64_t q) { return __uint_as_float((uint32_t)q); }
 __device__ __forceinline__ bool pair_has(uint64_t q, uint32_t tag) { return (uint32_t)(q >> 32) == tag; }
 
-// One round of a bounded poll: true once every lane is ready.  After
-// kSpinLimit rounds, or once another wait has failed (the error word, read
-// every 8192 rounds, far beyond any wait of a healthy launch), it records an
-// error and lets the wave go on: its results are then wrong, but the launch
-// ends.
+// One round of a bounded poll: true once every lane is ready.  `spin` starts
+// at the wait's limit (FusedArgs::spin_limit rounds, tens of milliseconds by
+// default: real waits take microseconds) and counts down.  When it runs out,
+// or once another wait has failed (the error word, read every 8192 rounds), it
+// records an error and lets the wave go on with spin = 0 (expired()): the
+// waiter then takes NaN for the values it waited for, so every output that
+// depends on them is NaN, and the launch still ends.
 __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* ctl) {
   if (__all(ready)) return true;
-  ++spin;
-  if (spin > kSpinLimit || ((spin & 8191u) == 0u && ld_word(ctl + C_ERR) != 0u)) {
+  --spin;  // >= 1 before: a wait that is not ready has not expired yet
+  if (spin == 0u || ((spin & 8191u) == 0u && ld_word(ctl + C_ERR) != 0u)) {
     if (lane() == 0) st_word(ctl + C_ERR, 1u);
+    spin = 0u;
     return true;
   }
   __builtin_amdgcn_s_sleep(2);
   return false;
 }
+__device__ __forceinline__ bool expired(uint32_t spin) { return spin == 0u; }
 
 // Polls n tagged pairs p[i * stride] (i < n <= N, per lane) until all carry
 // `tag`; their values land in v[0..n).  It first probes only the first pair
@@ -130,8 +137,8 @@ __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* 
 // to hoist out of the task loop).
 template <int N>
 __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, uint32_t* ctl,
-                                           float (&v)[N]) {
-  uint32_t spin = 0;
+                                           uint32_t limit, float (&v)[N]) {
+  uint32_t spin = limit;
   while (!poll_done(pair_has(ld_pair(p), tag), spin, ctl)) {
   }
   for (;;) {
@@ -148,7 +155,11 @@ __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, in
       v[i] = pair_value(q[i]);
       ok = ok && pair_has(q[i], tag);
     }
-    if (poll_done(ok, spin, ctl)) return;
+    if (poll_done(ok, spin, ctl)) break;
+  }
+  if (expired(spin)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = __builtin_nanf("");
   }
 }
 
@@ -263,7 +274,7 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   const int l = lane();
   const uint64_t* src = A.logits + (blockIdx.x % kLogitCopies) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
   uint64_t q;
-  uint32_t spin = 0;
+  uint32_t spin = A.spin_limit;
   const bool wtrace = A.trace != nullptr && t == 0 && l == 0;
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 0] = (int64_t)wall_clock64();
   do {
@@ -271,7 +282,7 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   } while (!poll_done(pair_has(q, tag), spin, A.ctl));
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 1] = (int64_t)wall_clock64();
   const bool real = l < A.E;
-  const float v = real ? pair_value(q) : -__builtin_huge_valf();
+  const float v = real ? (expired(spin) ? __builtin_nanf("") : pair_value(q)) : -__builtin_huge_valf();
   const float m = tree_max(v);
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 3] = (int64_t)wall_clock64();
   const float ex = real ? uexp(v - m) : 0.0f;
@@ -509,7 +520,7 @@ __device__ __attribute__((always_inline)) void task_sfold(const KA FusedArgs& A,
   for (int p = 0; p < 2; ++p) {
     float v[kMaxG];
     poll_pairs<kMaxG>(A.p_sgu + ((int64_t)(k.a * 2 + p) * A.gh * A.B + r) * 64 + l, (int64_t)A.B * 64, A.gh, C.tag,
-                      A.ctl, v);
+                      A.ctl, A.spin_limit, v);
     float sum = 0.0f;
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g)
@@ -534,7 +545,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
     const int np = 2 * A.B;
     const uint64_t* src = A.hs + (int64_t)g * 128 + l;
     float v[kMaxP];
-    uint32_t spin = 0;
+    uint32_t spin = A.spin_limit;
     while (!poll_done(pair_has(ld_pair(src), C.tag), spin, A.ctl)) {
     }
     for (;;) {
@@ -553,6 +564,10 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
         ok = ok && pair_has(q[i], C.tag);
       }
       if (poll_done(ok, spin, A.ctl)) break;
+    }
+    if (expired(spin)) {
+#pragma unroll
+      for (int i = 0; i < kMaxP; ++i) v[i] = __builtin_nanf("");
     }
 #pragma unroll
     for (int i = 0; i < kMaxP; ++i)
@@ -650,7 +665,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     const uint64_t* src = A.h + (int64_t)r * A.F + l;
     for (int i0 = 0; i0 < npairs; i0 += kMaxP) {
       float v[kMaxP];
-      poll_pairs<kMaxP>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl, v);
+      poll_pairs<kMaxP>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl, A.spin_limit, v);
 #pragma unroll
       for (int i = 0; i < kMaxP; ++i) {
         if (i0 + i < npairs) {
@@ -690,28 +705,34 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   const int l = lane();
   const int n = k.a * 64 + l;
   const int t = k.b;
+  // a failed earlier launch leaves the error word set: every output is then NaN until the host clears it
+  const uint32_t failed = ld_word(A.ctl + C_ERR);
   float v[kMaxG];
-  poll_pairs<kMaxG>(A.p_sdn + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag, A.ctl, v);
+  poll_pairs<kMaxG>(A.p_sdn + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag, A.ctl, A.spin_limit, v);
   float shv = 0.0f;
 #pragma unroll
   for (int g = 0; g < kMaxG; ++g)
     if (g < A.gfs) shv = shv + v[g];
   float y[kMaxK];
-  poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, y);
+  poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, A.spin_limit, y);
   UOCR_TRACE(A, C.t, 3);
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j)
     if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
-  A.out[(int64_t)t * A.H + n] = acc + shv;
+  A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : acc + shv;
   uint32_t old = 0;
   if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = shfl(old, 0);
   if (old + 1u == (uint32_t)A.n_comb) {
-    uint32_t spin = 0;
+    uint32_t spin = A.spin_limit;
     while (!poll_done(ld_word(A.ctl + C_ARRIVED) >= gridDim.x, spin, A.ctl)) {
     }
-    if (l == 0) {
+    // A workgroup that never arrived may still start: the counters and the
+    // epoch then stay as they are (that late workgroup takes this launch's
+    // tag), and the error word keeps later launches' outputs NaN until the
+    // host clears the slot.
+    if (l == 0 && !expired(spin)) {
       st_word(A.ctl + C_ARRIVED, 0u);
       st_word(A.ctl + C_COMBINED, 0u);
       st_word(A.ctl + C_EPOCH, epoch + 1u);
@@ -818,13 +839,14 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   int64_t troute = 0;
   for (;; t += nwaves) {
     if (!routed && t >= n_tasks) {
-      uint32_t spin = 0;
+      uint32_t spin = A.spin_limit;
       while (!poll_done(__hip_atomic_load(r_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= A.B, spin,
                         A.ctl)) {
       }
       asm volatile("" ::: "memory");
       if (A.trace != nullptr) troute = (int64_t)wall_clock64();
-      rt = make_route(A, r_ids);
+      // without the routing (a failed wait), no routed task runs: the combine's waits for them fail too
+      rt = expired(spin) ? Route{0ull, 0, r_ids, 0} : make_route(A, r_ids);
       n_tasks = task_count(A, rt.ng);
       routed = true;
     }

@@ -66,6 +66,35 @@ __global__ void __launch_bounds__(256) k_dequant(void* __restrict__ out, int out
   }
 }
 
+// ------------------------------------------------------------- quantiser
+//
+// Symmetric per-group int8 along K (tools/quantize_int8.py:54-70,298-329): one
+// wave per (row, group): amax = max |w| over the group (exact in any order),
+// scale = amax / 127 (1.0 for an all-zero group), q = clip(rint(w / scale),
+// +-127), every division correctly rounded fp32 and rint half to even -- the
+// reference's numpy arithmetic, bit for bit.
+
+__global__ void __launch_bounds__(256) k_quantize(int8_t* __restrict__ q, float* __restrict__ scales,
+                                                  const void* __restrict__ w, int w_bf16, int64_t groups_total,
+                                                  int group) {
+  const int64_t gi = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gi >= groups_total) return;
+  const int l = lane_id();
+  const int64_t base = gi * group;
+  auto value = [&](int64_t i) -> float {
+    return w_bf16 ? __uint_as_float((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i];
+  };
+  float amax = 0.0f;
+  for (int i = l; i < group; i += kWave) amax = fmaxf(amax, fabsf(value(base + i)));
+  amax = tree_max(amax);
+  const float s = amax == 0.0f ? 1.0f : amax / 127.0f;
+  for (int i = l; i < group; i += kWave) {
+    const float r = __builtin_rintf(value(base + i) / s);
+    q[base + i] = (int8_t)(int)fminf(fmaxf(r, -127.0f), 127.0f);
+  }
+  if (l == 0) scales[gi] = s;
+}
+
 // ------------------------------------------------------------- grouped GEMM
 //
 // A workgroup owns a BM-row tile of one expert's rows (or of the tokens, for
@@ -220,15 +249,26 @@ __device__ __forceinline__ Cursor make_cursor(const GemmProblem& P, const TileRe
   return c;
 }
 
-// Loads one K step at the cursor into registers.
-template <int BM, WKind W, int NPROJ>
+// 16 weight bytes at any alignment (the caller's stack may start anywhere):
+// the compiler splits the copy into loads the pointer's alignment allows.
+__device__ __forceinline__ i32x4 ld16_any(const char* p) {
+  i32x4 v;
+  __builtin_memcpy(&v, (const UOCR_GLOBAL char*)p, 16);
+  return v;
+}
+
+// Loads one K step at the cursor into registers.  VEC: the weights are
+// 16-byte aligned (one 16-byte load per piece); else each piece is read at
+// whatever alignment it has -- the same bytes either way.
+template <int BM, WKind W, int NPROJ, bool VEC>
 __device__ __forceinline__ void load_step(const Cursor& c, StepRegs<BM, W>& R) {
   using S = StepRegs<BM, W>;
 #pragma unroll
   for (int i = 0; i < S::kABytes / 16; ++i) R.a[i] = *(const UOCR_GLOBAL i32x4*)(c.a + 8 * i);
   constexpr int NB = S::kBBytes / 16;
 #pragma unroll
-  for (int i = 0; i < NB; ++i) R.b[i] = *(const UOCR_GLOBAL i32x4*)(c.b + 16 * i);
+  for (int i = 0; i < NB; ++i)
+    R.b[i] = VEC ? *(const UOCR_GLOBAL i32x4*)(c.b + 16 * i) : ld16_any(c.b + 16 * i);
   if constexpr (W == kInt8Rows) R.scale = ldg(c.s);
 }
 
@@ -304,7 +344,7 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
-template <int BM, WKind W, int NPROJ>
+template <int BM, WKind W, int NPROJ, bool VEC>
 __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds) {
   using S = StepRegs<BM, W>;
   uint16_t* As = lds;               // [BM][kRow]
@@ -337,13 +377,13 @@ __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds)
   // do not wait for it).
   S R;
   const int ksteps = P.K / BK;
-  load_step<BM, W, NPROJ>(cur, R);
+  load_step<BM, W, NPROJ, VEC>(cur, R);
   advance<W>(P, cur, ksteps > 1);
   for (int ks = 0; ks < ksteps; ++ks) {
     if (ks > 0) lds_barrier();
     store_step<BM, W>(R, As, Bs);
     if (ks + 1 < ksteps) {
-      load_step<BM, W, NPROJ>(cur, R);
+      load_step<BM, W, NPROJ, VEC>(cur, R);
       advance<W>(P, cur, ks + 2 < ksteps);
     }
     lds_barrier();
@@ -376,7 +416,7 @@ __device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds)
   }
 }
 
-template <int BM, WKind W0, int NP, WKind W1>
+template <int BM, WKind W0, int NP, WKind W1, bool VEC>
 __global__ void __launch_bounds__(Geo<BM>::kThreads) k_gemm_pair(GemmProblem a, GemmProblem b, int split) {
   extern __shared__ uint16_t lds[];
   constexpr int bn = kBRows / NP;
@@ -384,15 +424,15 @@ __global__ void __launch_bounds__(Geo<BM>::kThreads) k_gemm_pair(GemmProblem a, 
   if (wg < split) {
     const TileRef t = locate<BM>(a, wg, bn);
     if (!t.valid) return;
-    gemm_tile<BM, W0, NP>(a, t, lds);
+    gemm_tile<BM, W0, NP, VEC>(a, t, lds);
   } else {
     const TileRef t = locate<BM>(b, wg - split, bn);
     if (!t.valid) return;
-    gemm_tile<BM, W1, NP>(b, t, lds);
+    gemm_tile<BM, W1, NP, VEC>(b, t, lds);
   }
 }
 
-template <int BM, WKind W0, int NP>
+template <int BM, WKind W0, int NP, bool VEC = true>
 hipError_t launch_pair_bm(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles, hipStream_t s,
                           const char* name) {
   constexpr int bn = kBRows / NP;
@@ -401,7 +441,7 @@ hipError_t launch_pair_bm(const GemmProblem& routed, const GemmProblem& shared, 
   const int wgs = split + shared_wgs;
   if (wgs == 0) return hipSuccess;
   const size_t lds = (size_t)(BM + kBRows) * kRow * sizeof(uint16_t);
-  UOCR_LAUNCH(name, (k_gemm_pair<BM, W0, NP, kBf16KBlocked>), dim3(wgs), dim3(Geo<BM>::kThreads), lds, s, routed,
+  UOCR_LAUNCH(name, (k_gemm_pair<BM, W0, NP, kBf16KBlocked, VEC>), dim3(wgs), dim3(Geo<BM>::kThreads), lds, s, routed,
               shared, split);
   return hipGetLastError();
 }
@@ -418,12 +458,28 @@ hipError_t launch_dequant(void* out, int out_f32, const int8_t* w, const float* 
   return hipGetLastError();
 }
 
+hipError_t launch_quantize(int8_t* q, float* scales, const void* w, int w_bf16, int64_t groups_total, int group,
+                           hipStream_t s) {
+  if (groups_total == 0) return hipSuccess;
+  UOCR_LAUNCH("quantize", k_quantize, dim3((unsigned)((groups_total + 3) / 4)), dim3(256), 0, s, q, scales, w, w_bf16,
+              groups_total, group);
+  return hipGetLastError();
+}
+
 int gemm_bk() { return BK; }
 
 hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
-                            hipStream_t s) {
+                            hipStream_t s, bool vec) {
   const bool gu = routed.swiglu != 0;
   const char* name = gu ? "gemm_gateup" : "gemm_down";
+  if (!vec) {  // weights at any alignment: 64-row tiles only
+    if (bm != 64) return hipErrorInvalidValue;
+    if (routed.kind == kInt8Rows)
+      return gu ? launch_pair_bm<64, kInt8Rows, 2, false>(routed, shared, max_mtiles, s, name)
+                : launch_pair_bm<64, kInt8Rows, 1, false>(routed, shared, max_mtiles, s, name);
+    return gu ? launch_pair_bm<64, kBf16Rows, 2, false>(routed, shared, max_mtiles, s, name)
+              : launch_pair_bm<64, kBf16Rows, 1, false>(routed, shared, max_mtiles, s, name);
+  }
   if (bm == 128) {
     if (routed.kind == kInt8Rows)
       return gu ? launch_pair_bm<128, kInt8Rows, 2>(routed, shared, max_mtiles, s, name)

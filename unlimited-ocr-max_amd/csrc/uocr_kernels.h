@@ -134,6 +134,9 @@ hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* 
 
 // ---- int8 dequantisation and the prefill grouped GEMM (gemm.hip) ----
 
+// q int8 [groups_total * group], scales fp32 [groups_total] from w fp32 or bf16 bits.
+hipError_t launch_quantize(int8_t* q, float* scales, const void* w, int w_bf16, int64_t groups_total, int group,
+                           hipStream_t s);
 hipError_t launch_dequant(void* out, int out_f32, const int8_t* w, const float* scales, const int32_t* idx,
                           int E, int N, int K, int groups, int vec, hipStream_t s);
 
@@ -162,8 +165,10 @@ struct GemmProblem {
   int out_by_position;        // 1: output row = position in group order, 0: row id
 };
 // bm: rows per tile, 64 or 128 (must match the group tables' tile_start).
+// vec: every weight pointer is 16-byte aligned; else the weights are read at
+// any alignment (bm must be 64), with the same bits.
 hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
-                            hipStream_t s);
+                            hipStream_t s, bool vec = true);
 
 // ---- the n-gram logit guard (ngram.hip) ----
 
@@ -267,6 +272,8 @@ struct FusedArgs {
   // layout (FusedLayout)
   int gh, gf, gfs, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, n_sfold, n_comb, lds_x, lds_act;
   float inv_gh, inv_gf;
+  // polls a wait may take before it fails (sets the error word, takes NaN)
+  uint32_t spin_limit;
   // optional per-task phase timestamps (8 words per task), null when off;
   // per-workgroup words start at trace_wg
   int64_t* trace;

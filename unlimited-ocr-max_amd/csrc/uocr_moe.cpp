@@ -88,6 +88,7 @@ struct CachedBuffer {
 
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, CachedBuffer> g_ws;
+std::vector<void*> g_retired;  // superseded library workspaces (freed by uocr_moe_release)
 
 // The library's own workspace for (current device, stream), at least `bytes`.
 hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
@@ -98,9 +99,8 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
   CachedBuffer& b = g_ws[{dev, stream}];
   if (b.bytes < bytes) {
     if (b.ptr != nullptr) {
-      e = hipStreamSynchronize(stream);  // work still queued may use the old buffer
-      if (e != hipSuccess) return e;
-      (void)hipFree(b.ptr);
+      // queued work or a captured graph may still use the old buffer: it lives until uocr_moe_release
+      g_retired.push_back(b.ptr);
       b.ptr = nullptr;
       b.bytes = 0;
     }
@@ -113,24 +113,26 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
   return hipSuccess;
 }
 
-// State of the persistent decode kernel: per device, kFusedSlots slots of
-// control words and tagged buffers, allocated and zeroed by the first call on
-// the device (which must not be under stream capture, and neither may a later
-// call whose layer needs more room); each stream takes a slot when first seen
-// (round robin), so streams first seen under capture need no allocation.
-// Launches on streams that share a slot must not overlap in time.
+// State of the persistent decode kernel.  Each (device, stream) owns one slot:
+// kFusedCtlWords control words and a tagged-data arena sized for the largest
+// layer the persistent path accepts (fused_max_words), zeroed when allocated.
+// Slots come in chunks of kFusedChunk, allocated by calls outside stream
+// capture; a stream first seen under capture takes a spare slot, or the call is
+// refused.  No slot is shared by two streams, and nothing is freed before
+// uocr_moe_release(), so graphs captured earlier keep valid pointers.
 constexpr int kFusedCtlWords = 64;
-constexpr int kFusedSlots = 16;
+constexpr int kFusedChunk = 4;
+constexpr int C_ERR_WORD = 4;  // the kernel's error word (decode.hip)
 struct FusedSlot {
   uint32_t* ctl = nullptr;
   uint64_t* data = nullptr;
 };
 struct FusedDevice {
-  uint32_t* ctl = nullptr;   // kFusedSlots x kFusedCtlWords
-  uint64_t* data = nullptr;  // kFusedSlots x words
-  int64_t words = 0;
-  int next = 0;
-  std::map<hipStream_t, int> slot;
+  std::vector<void*> chunks;
+  std::vector<FusedSlot> spare;
+  std::map<hipStream_t, FusedSlot> slot;
+  hipStream_t last_stream = nullptr;  // stream of the last eager persistent launch
+  hipEvent_t handoff = nullptr;       // orders eager launches on different streams
 };
 std::map<int, FusedDevice> g_fused;
 std::map<std::pair<int, size_t>, int> g_fused_grid;  // (device, LDS bytes) -> workgroups
@@ -145,57 +147,79 @@ bool capturing(hipStream_t stream) {
   return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
-// The slot of (current device, stream) with room for `data_words` tagged
-// words; *need_alloc is set when that needs an allocation under capture.
-hipError_t fused_slot(hipStream_t stream, int64_t data_words, FusedSlot* out, bool* need_alloc) {
+// Tagged words of the largest layer the persistent path takes (8 tokens, top-8,
+// 64 experts, every width 2048): every slot has room for any eligible layer.
+int64_t fused_max_words() { return fused_layout(8, 64, 2048, 2048, 2048, 8).data_words; }
+size_t fused_slot_bytes() { return ((size_t)kFusedCtlWords * 4 + (size_t)fused_max_words() * 8 + 255) & ~size_t(255); }
+
+// A new chunk of zeroed slots (g_ws_mu held, not under capture).
+hipError_t fused_grow(FusedDevice& d, hipStream_t stream) {
+  const size_t bytes = kFusedChunk * fused_slot_bytes();
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return e;
+  e = launch_zero_words(static_cast<uint32_t*>(p), (int64_t)(bytes / 4), stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);  // zero before any stream uses a slot
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return e;
+  }
+  d.chunks.push_back(p);
+  for (int i = kFusedChunk - 1; i >= 0; --i) {
+    char* base = static_cast<char*>(p) + (size_t)i * fused_slot_bytes();
+    d.spare.push_back(FusedSlot{reinterpret_cast<uint32_t*>(base),
+                                reinterpret_cast<uint64_t*>(base + (size_t)kFusedCtlWords * 4)});
+  }
+  return hipSuccess;
+}
+
+// The slot of (current device, stream); *need_alloc is set when the stream is
+// new and no spare slot is left under capture.
+hipError_t fused_slot(hipStream_t stream, FusedSlot* out, bool* need_alloc) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(g_ws_mu);
   FusedDevice& d = g_fused[dev];
   *need_alloc = false;
-  if (d.ctl == nullptr || d.words < data_words) {
-    if (capturing(stream)) {
+  auto it = d.slot.find(stream);
+  if (it != d.slot.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  const bool cap = capturing(stream);
+  if (d.spare.empty()) {
+    if (cap) {
       *need_alloc = true;
       return hipSuccess;
     }
-    e = hipDeviceSynchronize();  // queued launches may still use the old buffers
-    if (e != hipSuccess) return e;
-    if (d.ctl == nullptr) {
-      e = hipMalloc(&d.ctl, (size_t)kFusedSlots * kFusedCtlWords * sizeof(uint32_t));
-      if (e != hipSuccess) {
-        d.ctl = nullptr;
-        return e;
-      }
-      e = launch_zero_words(d.ctl, (int64_t)kFusedSlots * kFusedCtlWords, stream);
-      if (e != hipSuccess) return e;
-    }
-    if (d.words < data_words) {
-      if (d.data != nullptr) (void)hipFree(d.data);
-      d.data = nullptr;
-      d.words = 0;
-      e = hipMalloc(&d.data, (size_t)kFusedSlots * data_words * sizeof(uint64_t));
-      if (e != hipSuccess) {
-        d.data = nullptr;
-        return e;
-      }
-      e = launch_zero_words(reinterpret_cast<uint32_t*>(d.data), 2 * kFusedSlots * data_words, stream);
-      if (e != hipSuccess) return e;
-      d.words = data_words;
-    }
-    e = hipStreamSynchronize(stream);
+    e = fused_grow(d, stream);
     if (e != hipSuccess) return e;
   }
-  int k;
-  auto it = d.slot.find(stream);
-  if (it == d.slot.end()) {
-    k = d.next++ % kFusedSlots;
-    d.slot[stream] = k;
-  } else {
-    k = it->second;
+  *out = d.spare.back();
+  d.spare.pop_back();
+  d.slot[stream] = *out;
+  // keep a spare for a stream that first appears under capture
+  if (d.spare.empty() && !cap) e = fused_grow(d, stream);
+  return e;
+}
+
+// Eager persistent launches need the whole device: one on another stream than
+// the previous one first waits for everything queued on that stream.
+hipError_t fused_order(hipStream_t stream) {
+  if (capturing(stream)) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  FusedDevice& d = g_fused[dev];
+  if (d.last_stream != nullptr && d.last_stream != stream) {
+    if (d.handoff == nullptr) e = hipEventCreateWithFlags(&d.handoff, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(d.handoff, d.last_stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(stream, d.handoff, 0);
+    if (e != hipSuccess) return e;
   }
-  out->ctl = d.ctl + (size_t)k * kFusedCtlWords;
-  out->data = d.data + (size_t)k * d.words;
+  d.last_stream = stream;
   return hipSuccess;
 }
 
@@ -351,6 +375,21 @@ int uocr_int8_dequant_expert(void* result, int64_t result_n, int64_t result_kdim
   const hipError_t e = launch_dequant(result, result_f32, w, scales, expert_idx, (int)w_e, (int)w_n, (int)w_kdim,
                                       (int)s_groups, vec, (hipStream_t)stream);
   return e == hipSuccess ? 0 : hip_fail(err, errlen, "int8_dequant_expert", e);
+}
+
+int uocr_quantize_per_group(int8_t* q, float* scales, const void* w, int w_bf16, int64_t rows, int64_t kdim,
+                            int64_t group, void* stream, char* err, size_t errlen) {
+  // tools/quantize_int8.py:306-310
+  if (group < 1 || group > (1 << 20)) return fail(err, errlen, "quantize_per_group: bad group size %lld", (long long)group);
+  if (rows < 0 || kdim < 0) return fail(err, errlen, "quantize_per_group: bad shape [%lld, %lld]", (long long)rows,
+                                        (long long)kdim);
+  if (kdim % group)
+    return fail(err, errlen, "quantize_per_group: K=%lld is not divisible by the group size %lld", (long long)kdim,
+                (long long)group);
+  if (rows == 0 || kdim == 0) return 0;
+  if (!q || !scales || !w) return fail(err, errlen, "quantize_per_group: a tensor is missing");
+  const hipError_t e = launch_quantize(q, scales, w, w_bf16 != 0, rows * (kdim / group), (int)group, (hipStream_t)stream);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, "quantize_per_group", e);
 }
 
 int uocr_dense_bf16_qmv(float* result, int64_t result_m, int64_t result_n, const float* x, int64_t x_m,
@@ -713,6 +752,18 @@ static bool fused_eligible(const uocr_moe_layer* L, int64_t B) {
   return lay.lds_bytes <= kMaxLds;
 }
 
+// Polls per bounded wait of the persistent kernel: 2^16 (tens of milliseconds;
+// healthy waits take microseconds).  UOCR_MOE_SPIN_LIMIT (>= 1) overrides it, so
+// a test can make the waits run out and check the failure path.
+static uint32_t fused_spin_limit() {
+  const char* env = std::getenv("UOCR_MOE_SPIN_LIMIT");
+  if (env != nullptr) {
+    const long v = std::strtol(env, nullptr, 10);
+    if (v >= 1 && v <= (1L << 30)) return (uint32_t)v;
+  }
+  return 1u << 16;
+}
+
 static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayout& lay, const FusedSlot& f) {
   FusedArgs a{};
   a.B = (int)B;
@@ -757,6 +808,7 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.lds_act = lay.lds_act;
   a.inv_gh = 1.0f / (float)lay.gh;
   a.inv_gf = 1.0f / (float)lay.gf;
+  a.spin_limit = fused_spin_limit();
   return a;
 }
 
@@ -825,26 +877,35 @@ int uocr_moe_gate(int64_t* indices, float* weights, const float* x, int64_t seq,
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
 
-int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidden, const uocr_moe_layer* L,
-                         int32_t* expert_ids, float* expert_weights, void* workspace, size_t workspace_bytes,
-                         void* stream, char* err, size_t errlen) {
-  const char* op = "uocr_moe_decode_rows";
+}  // extern "C"
+
+// The decode layer.  fixed: the persistent kernel's control words and arena,
+// given by the caller; null: the stream's own slot.
+static int decode_rows_impl(const char* op, float* out, const float* x, int64_t rows, int64_t hidden,
+                            const uocr_moe_layer* L, int32_t* expert_ids, float* expert_weights, void* workspace,
+                            size_t workspace_bytes, hipStream_t s, const FusedSlot* fixed, char* err,
+                            size_t errlen) {
   if (check_layer(op, L, hidden, err, errlen)) return 1;
   if (rows < 0 || rows > 64) return fail(err, errlen, "%s: rows must be in [0, 64]", op);
   if (rows == 0) return 0;
-  const hipStream_t s = (hipStream_t)stream;
   const int64_t B = rows, R = rows * L->top_k;
   if (fused_eligible(L, B)) {
     const FusedLayout lay = fused_layout((int)B, (int)L->num_experts, (int)L->hidden, (int)L->ffn,
                                          (int)L->shared_ffn, (int)L->top_k);
     FusedSlot slot;
-    bool need_alloc = false;
-    hipError_t e = fused_slot(s, lay.data_words, &slot, &need_alloc);
-    if (e == hipSuccess && need_alloc)
-      return fail(err, errlen,
-                  "%s: the first decode call on a device (or the first with a larger layer) must not be under "
-                  "stream capture",
-                  op);
+    hipError_t e = hipSuccess;
+    if (fixed != nullptr) {
+      slot = *fixed;
+    } else {
+      bool need_alloc = false;
+      e = fused_slot(s, &slot, &need_alloc);
+      if (e == hipSuccess && need_alloc)
+        return fail(err, errlen,
+                    "%s: no free control slot for a new stream under capture (make a decode call on this device "
+                    "outside stream capture first; it keeps a spare slot ready)",
+                    op);
+      if (e == hipSuccess) e = fused_order(s);
+    }
     int grid = 0;
     if (e == hipSuccess) e = fused_grid_cached(lay.lds_bytes, &grid);
     if (e != hipSuccess) return hip_fail(err, errlen, op, e);
@@ -854,7 +915,7 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
     a.out = out;
     a.ids_out = expert_ids;
     a.wts_out = expert_weights;
-    {
+    if (fixed == nullptr) {
       std::lock_guard<std::mutex> lock(g_ws_mu);
       if (g_trace != nullptr && g_trace_words >= ((int64_t)lay.max_tasks + grid) * 8) {
         a.trace = g_trace;
@@ -965,6 +1026,15 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
 
+extern "C" {
+
+int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidden, const uocr_moe_layer* L,
+                         int32_t* expert_ids, float* expert_weights, void* workspace, size_t workspace_bytes,
+                         void* stream, char* err, size_t errlen) {
+  return decode_rows_impl("uocr_moe_decode_rows", out, x, rows, hidden, L, expert_ids, expert_weights, workspace,
+                          workspace_bytes, (hipStream_t)stream, nullptr, err, errlen);
+}
+
 int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, const uocr_moe_layer* L,
                      int32_t* expert_ids, float* expert_weights, void* workspace, size_t workspace_bytes,
                      void* stream, char* err, size_t errlen) {
@@ -975,14 +1045,17 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
     return fail(err, errlen, "%s: hidden, ffn and shared_ffn must be multiples of %d", op, BK);
   if (L->int8 && (L->group % 64 || BK % L->group != 0 && L->group % BK != 0))
     return fail(err, errlen, "%s: the int8 group must be 64, 128 or a multiple of 128", op);
-  if (!aligned16(x) || !aligned16(L->gate_proj) || !aligned16(L->up_proj) || !aligned16(L->down_proj) ||
-      !aligned16(L->shared_gate) || !aligned16(L->shared_up) || !aligned16(L->shared_down))
-    return fail(err, errlen, "%s: x and the weights must be 16-byte aligned", op);
+  // x is read by scalar loads; the weights by 16-byte loads when every stack is 16-byte aligned, else by
+  // loads of whatever width their alignment allows (the same bits; the reference picks its load path the
+  // same way, unlimited_ocr_max/kernels/loads.mojo:59-89)
+  const bool vec = aligned16(L->gate_proj) && aligned16(L->up_proj) && aligned16(L->down_proj) &&
+                   aligned16(L->shared_gate) && aligned16(L->shared_up) && aligned16(L->shared_down);
+  if ((reinterpret_cast<uintptr_t>(x) & 3u) != 0) return fail(err, errlen, "%s: x must be 4-byte aligned", op);
   if (seq < 0 || seq * L->top_k > ((int64_t)1 << 28)) return fail(err, errlen, "%s: seq out of range", op);
   if (seq == 0) return 0;
   const hipStream_t s = (hipStream_t)stream;
   const int64_t T = seq, R = seq * L->top_k;
-  const int BM = R >= 8192 ? 128 : 64;  // rows per GEMM tile
+  const int BM = R >= 8192 && vec ? 128 : 64;  // rows per GEMM tile
   Carve dry(nullptr);
   carve_prefill(dry, L, T);
   void* ws = nullptr;
@@ -1042,7 +1115,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sgu.swiglu = 1;
   sgu.outb = d.hsb;
   sgu.ldo = Fs;
-  e = launch_gemm_pair(gu, sgu, BM, max_mtiles, s);
+  e = launch_gemm_pair(gu, sgu, BM, max_mtiles, s, vec);
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
 
   GemmProblem dn = gu;
@@ -1072,7 +1145,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sdn.outb = nullptr;
   sdn.outf = d.sh;
   sdn.ldo = H;
-  e = launch_gemm_pair(dn, sdn, BM, max_mtiles, s);
+  e = launch_gemm_pair(dn, sdn, BM, max_mtiles, s, vec);
   if (e == hipSuccess) e = launch_combine(out, d.y, H, d.wts, d.g.inv, d.sh, (int)T, H, (int)L->top_k, s);
   if (e == hipSuccess && expert_ids) e = hipMemcpyAsync(expert_ids, d.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
   if (e == hipSuccess && expert_weights)
@@ -1128,23 +1201,34 @@ int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err
 }
 
 int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen) {
+  const hipStream_t s = (hipStream_t)stream;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  uint32_t* ctl = nullptr;
+  // the stream's slot (control words, then the tagged arena)
+  std::vector<std::pair<uint32_t*, int64_t>> areas;
   if (e == hipSuccess) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     auto it = g_fused.find(dev);
-    if (it != g_fused.end() && it->second.ctl != nullptr) {
-      auto sl = it->second.slot.find((hipStream_t)stream);
-      if (sl != it->second.slot.end()) ctl = it->second.ctl + (size_t)sl->second * kFusedCtlWords;
+    if (it != g_fused.end()) {
+      auto sl = it->second.slot.find(s);
+      if (sl != it->second.slot.end()) areas.emplace_back(sl->second.ctl, (int64_t)(fused_slot_bytes() / 4));
     }
   }
-  uint32_t v = 0;
-  if (e == hipSuccess && ctl != nullptr)
-    e = hipMemcpyAsync(&v, ctl + 4, sizeof(v), hipMemcpyDeviceToHost, (hipStream_t)stream);
-  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  uint32_t v[2] = {0u, 0u};
+  for (size_t i = 0; e == hipSuccess && i < areas.size(); ++i)
+    e = hipMemcpyAsync(&v[i], areas[i].first + C_ERR_WORD, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  // a failed launch leaves its slot poisoned (outputs NaN): clear it, control words and tags alike
+  bool cleared = false;
+  for (size_t i = 0; e == hipSuccess && i < areas.size(); ++i) {
+    if (v[i] != 0u) {
+      e = launch_zero_words(areas[i].first, areas[i].second, s);
+      cleared = true;
+    }
+  }
+  if (e == hipSuccess && cleared) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_fail(err, errlen, "uocr_moe_fused_errors", e);
-  if (errors) *errors = v;
+  if (errors) *errors = (v[0] | v[1]) != 0u ? 1u : 0u;
   return 0;
 }
 
@@ -1153,9 +1237,11 @@ void uocr_moe_release(void) {
   for (auto& kv : g_ws)
     if (kv.second.ptr != nullptr) (void)hipFree(kv.second.ptr);
   g_ws.clear();
+  for (void* p : g_retired) (void)hipFree(p);
+  g_retired.clear();
   for (auto& kv : g_fused) {
-    if (kv.second.ctl != nullptr) (void)hipFree(kv.second.ctl);
-    if (kv.second.data != nullptr) (void)hipFree(kv.second.data);
+    for (void* p : kv.second.chunks) (void)hipFree(p);
+    if (kv.second.handoff != nullptr) (void)hipEventDestroy(kv.second.handoff);
   }
   g_fused.clear();
   g_fused_grid.clear();

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, list] = {
     "uocr_moe_bf16_qmv": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp, _cp, _sz],
     "uocr_int8_dequant_expert": [_vp, _i64, _i64, _int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64,
                                  _vp, _cp, _sz],
+    "uocr_quantize_per_group": [_vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _cp, _sz],
     "uocr_dense_bf16_qmv": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _cp, _sz],
     "uocr_ngram_block": [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _cp, _sz],
     "uocr_paged_decode_attention_qkv": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64,
@@ -119,7 +120,8 @@ def timing_end(capacity: int) -> list[tuple[str, float]]:
 
 
 def fused_errors(stream: int | None = None) -> int:
-    """Synchronises ``stream`` (default: torch's current) and returns the persistent decode kernel's error word."""
+    """Synchronises ``stream`` (default: torch's current) and returns the persistent decode kernel's error word
+    (1: a launch ran out of its bounded waits; its slot, poisoned until now, is cleared by this call)."""
     import torch
 
     if stream is None:

@@ -21,7 +21,8 @@ step metadata as a :class:`PagedKv`.
 
 :func:`custom` dispatches by symbol like ``ops.custom(symbol, values=...)``.
 Inputs must be GPU tensors; non-contiguous views are packed first (the
-reference reads strided inputs with the same bits as packed ones).  Work is
+reference reads strided inputs with the same bits as packed ones).  An
+``out=`` tensor is written in place and must be contiguous.  Work is
 enqueued on the current torch stream.
 """
 
@@ -57,6 +58,15 @@ def _gpu(op: str, name: str, t: torch.Tensor, dtype: torch.dtype, rank: int) -> 
     return t.contiguous()
 
 
+def _out(op: str, name: str, t: torch.Tensor, dtype: torch.dtype, rank: int) -> torch.Tensor:
+    """An output tensor: checked like an input, and written in place, so it must be contiguous (a packed
+    copy would take the result and leave the caller's tensor unchanged)."""
+    _gpu(op, name, t, dtype, rank)
+    if not t.is_contiguous():
+        raise ValueError(f"{op}: {name} must be contiguous (the result is written into it in place)")
+    return t
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -85,7 +95,7 @@ def moe_int8_qmv(x, expert_ids, w, scales, *, out: torch.Tensor | None = None) -
     scales = _gpu(op, "scales", scales, torch.float32, 3)
     if out is None:
         out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
-    out = _gpu(op, "result", out, torch.float32, 2)
+    out = _out(op, "result", out, torch.float32, 2)
     _lib.call("uocr_moe_int8_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0], x.shape[1],
               expert_ids.data_ptr(), expert_ids.shape[0], w.data_ptr(), *w.shape, scales.data_ptr(), *scales.shape,
               _stream(x))
@@ -100,7 +110,7 @@ def moe_bf16_qmv(x, expert_ids, w, *, out: torch.Tensor | None = None) -> torch.
     w = _gpu(op, "w", w, torch.bfloat16, 3)
     if out is None:
         out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
-    out = _gpu(op, "result", out, torch.float32, 2)
+    out = _out(op, "result", out, torch.float32, 2)
     _lib.call("uocr_moe_bf16_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0], x.shape[1],
               expert_ids.data_ptr(), expert_ids.shape[0], w.data_ptr(), *w.shape, _stream(x))
     return out
@@ -120,7 +130,7 @@ def int8_dequant_expert(w, scales, expert_idx, *, dtype: torch.dtype = torch.bfl
         out = torch.empty((w.shape[1], w.shape[2]), dtype=dtype, device=w.device)
     if out.dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"{op}: the result must be bfloat16 or float32, got {out.dtype}")
-    out = _gpu(op, "result", out, out.dtype, 2)
+    out = _out(op, "result", out, out.dtype, 2)
     _lib.call("uocr_int8_dequant_expert", out.data_ptr(), out.shape[0], out.shape[1], int(out.dtype == torch.float32),
               w.data_ptr(), *w.shape, scales.data_ptr(), *scales.shape, expert_idx.data_ptr(), expert_idx.shape[0],
               _stream(w))
@@ -139,7 +149,7 @@ def dense_bf16_qmv(x, w, *, tile: int | None = None, out: torch.Tensor | None = 
         tile = _rows_per_read(int(x.shape[0]), int(w.shape[1]))
     if out is None:
         out = torch.empty((x.shape[0], w.shape[1]), dtype=torch.float32, device=x.device)
-    out = _gpu(op, "result", out, torch.float32, 2)
+    out = _out(op, "result", out, torch.float32, 2)
     _lib.call("uocr_dense_bf16_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0], x.shape[1],
               w.data_ptr(), *w.shape, int(tile), _stream(x))
     return out
@@ -167,7 +177,7 @@ def ngram_block(logits, history, ngram, *, out: torch.Tensor | None = None) -> t
     ngram = _gpu(op, "ngram", ngram, torch.int32, 1)
     if out is None:
         out = torch.empty_like(logits)
-    out = _gpu(op, "result", out, torch.float32, rank)
+    out = _out(op, "result", out, torch.float32, rank)
     rows = 1 if rank == 1 else int(logits.shape[0])
     hrows = 1 if rank == 1 else int(history.shape[0])
     orows = 1 if rank == 1 else int(out.shape[0])
@@ -198,7 +208,7 @@ def rms_norm(x, gamma, eps: float, *, residual=None, out: torch.Tensor | None = 
             raise ValueError(f"{op}: x_out must be a contiguous {tuple(x.shape)} tensor")
     if out is None:
         out = torch.empty_like(x)
-    out = _gpu(op, "out", out, torch.float32, 2)
+    out = _out(op, "out", out, torch.float32, 2)
     if out.shape != x.shape:
         raise ValueError(f"{op}: out must be {tuple(x.shape)}")
     _lib.call("uocr_rms_norm", out.data_ptr(), _ptr(x_out), x.data_ptr(), _ptr(residual), gamma.data_ptr(),
@@ -239,7 +249,7 @@ def rms_norm_dense_bf16_qmv(x, gamma, eps: float, w, *, residual=None, x_out=Non
             raise ValueError(f"{op}: residual and x_out must be contiguous {tuple(x.shape)} tensors")
     if out is None:
         out = torch.empty((x.shape[0], w.shape[1]), device=x.device, dtype=torch.float32)
-    out = _gpu(op, "result", out, torch.float32, 2)
+    out = _out(op, "result", out, torch.float32, 2)
     _lib.call("uocr_rms_norm_dense_bf16_qmv", out.data_ptr(), out.shape[0], out.shape[1], x.data_ptr(), x.shape[0],
               x.shape[1], _ptr(residual), _ptr(x_out), gamma.data_ptr(), float(eps), w.data_ptr(), w.shape[0],
               w.shape[1], w.shape[2], _stream(x))
@@ -291,7 +301,7 @@ def swiglu(gate_up, *, out: torch.Tensor | None = None) -> torch.Tensor:
     ffn = gate_up.shape[1] // 2
     if out is None:
         out = torch.empty((gate_up.shape[0], ffn), device=gate_up.device, dtype=torch.float32)
-    out = _gpu(op, "out", out, torch.float32, 2)
+    out = _out(op, "out", out, torch.float32, 2)
     if tuple(out.shape) != (gate_up.shape[0], ffn):
         raise ValueError(f"{op}: out must be {(gate_up.shape[0], ffn)}")
     _lib.call("uocr_swiglu", out.data_ptr(), gate_up.data_ptr(), gate_up.shape[0], ffn, _stream(gate_up))
@@ -357,7 +367,7 @@ def paged_decode_attention(q, k_new, v_new, *, kv: PagedKv, layer_idx: int, scal
         raise ValueError(f"{op}: the step metadata is not for {rows} rows")
     if out is None:
         out = torch.empty_like(q)
-    out = _gpu(op, "out", out, torch.float32, 3)
+    out = _out(op, "out", out, torch.float32, 3)
     if out.shape != q.shape:
         raise ValueError(f"{op}: out must be {tuple(q.shape)}, got {tuple(out.shape)}")
     ws, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
@@ -402,7 +412,7 @@ def paged_decode_attention_qkv(qkv, positions, cos_table, sin_table, *, heads: i
         raise ValueError(f"{op}: the step metadata is not for {rows} rows")
     if out is None:
         out = torch.empty((rows, heads, head_dim), device=qkv.device, dtype=torch.float32)
-    out = _gpu(op, "out", out, torch.float32, 3)
+    out = _out(op, "out", out, torch.float32, 3)
     ws, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
     _lib.call("uocr_paged_decode_attention_qkv", out.data_ptr(), qkv.data_ptr(), rows, heads, head_dim, qkv.stride(0),
               positions.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), cos_table.shape[0],
@@ -440,14 +450,24 @@ def kblocked(weight: torch.Tensor) -> torch.Tensor:
 
 
 def quantize_per_group(w: torch.Tensor, group: int = INT8_GROUP_SIZE) -> tuple[torch.Tensor, torch.Tensor]:
-    """Symmetric per-group int8 of ``[..., K]`` along K (tools/quantize_int8.py:54-70,298-329):
-    ``scale = amax/127`` (1.0 for an all-zero group), ``q = clip(rint(w/scale), -127, 127)``, in fp32."""
-    wf = w.float()
-    k = wf.shape[-1]
+    """Symmetric per-group int8 of a GPU tensor ``[..., K]`` along K (tools/quantize_int8.py:54-70,298-329):
+    ``scale = amax/127`` (1.0 for an all-zero group), ``q = clip(rint(w/scale), -127, 127)``, in fp32 with
+    correctly rounded divisions (bitwise the reference's numpy) -> ``(int8 [..., K], fp32 [..., K/group])``.
+    bf16 and fp32 weights are read as they are; other float dtypes are converted to fp32 first."""
+    op = "quantize_per_group"
+    if not isinstance(w, torch.Tensor) or w.dim() < 1:
+        raise TypeError(f"{op}: w must be a torch.Tensor of rank >= 1")
+    k = int(w.shape[-1])
     if k % group:
         raise ValueError(f"K={k} is not divisible by the group size {group}")
-    grouped = wf.reshape(*wf.shape[:-1], k // group, group)
-    amax = grouped.abs().amax(dim=-1)
-    scales = torch.where(amax == 0, torch.ones_like(amax), amax / 127.0)
-    q = torch.round(grouped / scales[..., None]).clamp_(-127, 127)
-    return q.to(torch.int8).reshape(wf.shape).contiguous(), scales.contiguous()
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        w = w.float()
+    w = _gpu(op, "w", w, w.dtype, w.dim())
+    if not bool(torch.isfinite(w).all()):
+        raise ValueError("weight holds NaN or Inf; refusing to quantise it")
+    q = torch.empty(w.shape, dtype=torch.int8, device=w.device)
+    scales = torch.empty((*w.shape[:-1], k // group), dtype=torch.float32, device=w.device)
+    rows = w.numel() // k if k else 0
+    _lib.call("uocr_quantize_per_group", q.data_ptr(), scales.data_ptr(), w.data_ptr(), int(w.dtype == torch.bfloat16),
+              rows, k, group, _stream(w))
+    return q, scales
