@@ -127,3 +127,47 @@ def test_moe_from_checkpoint_decodes_like_the_direct_layer(oracle, small) -> Non
         x = t(oracle.rmsnorm_rows(np.random.default_rng(5), 3, 256))
         assert bits_equal(n(loaded.decode_rows(x)), n(direct.decode_rows(x)))
         assert bits_equal(n(loaded(x)), n(direct(x)))
+
+
+def test_stack_refusals_name_the_stack_in_the_reference_format(small) -> None:
+    """The texts tests/test_weight_adapters.py:120-147 match: the stack's name, then the reason with the
+    offending dtypes, shapes or counts listed in sorted order."""
+    p = f"model.layers.{LAYER}.mlp.experts."
+    bf = checkpoint_of(small[False])
+    mixed = dict(bf)
+    mixed[p + "2.up_proj.weight"] = mixed[p + "2.up_proj.weight"].float()
+    with pytest.raises(WeightMappingError) as info:
+        moe_layer_weights(mixed, LAYER, num_experts=4)
+    assert str(info.value) == f"layers.{LAYER}.mlp.experts.up_proj: the experts disagree on dtype: ['bfloat16', 'float32']"
+    half = dict(bf)
+    half[p + "2.up_proj.weight"] = half[p + "2.up_proj.weight"][:, :128].contiguous()
+    with pytest.raises(WeightMappingError) as info:
+        moe_layer_weights(half, LAYER, num_experts=4)
+    assert str(info.value) == f"layers.{LAYER}.mlp.experts.up_proj: the experts disagree on shape: [(128, 128), (128, 256)]"
+    ck = checkpoint_of(small[True])
+    short = {k: v for k, v in ck.items() if not k.startswith(p + "3.")}
+    with pytest.raises(WeightMappingError) as info:
+        moe_layer_weights(short, LAYER, num_experts=4)
+    assert str(info.value) == f"layers.{LAYER}.mlp.experts.gate_proj: expected 4 experts, got 3"
+    gap = {k: v for k, v in ck.items() if not k.startswith(p + "0.")}
+    with pytest.raises(WeightMappingError) as info:
+        moe_layer_weights(gap, LAYER, num_experts=4)
+    assert str(info.value) == (f"layers.{LAYER}.mlp.experts.gate_proj: expert indices must be 0..n-1 with no gaps, "
+                               "got [1, 2, 3]")
+
+
+def test_form_refusals_list_the_offenders(small) -> None:
+    """The four half-quantized refusals list the offending tensors by their checkpoint names (the first 20,
+    sorted), scales named with their suffix."""
+    p = f"model.layers.{LAYER}.mlp.experts."
+    ck = checkpoint_of(small[True])
+    orphan = {k: v for k, v in ck.items() if k not in (p + "2.gate_proj.weight", p + "0.up_proj.weight")}
+    with pytest.raises(WeightMappingError) as info:
+        is_int8_checkpoint(orphan)
+    assert str(info.value) == ("weight_scales without an expert weight to scale: "
+                               f"['{p}0.up_proj.weight_scales', '{p}2.gate_proj.weight_scales']")
+    bare = {k: v for k, v in ck.items() if k != p + "1.down_proj.weight_scales"}
+    with pytest.raises(WeightMappingError) as info:
+        is_int8_checkpoint(bare, LAYER)
+    assert str(info.value) == f"half-quantized checkpoint: no weight_scales for ['{p}1.down_proj.weight']"
+    assert not is_int8_checkpoint(ck, LAYER + 1)  # another layer holds no experts: nothing to judge

@@ -1,31 +1,41 @@
-"""Checkpoint tensors -> one MoE layer's weights (unlimited_ocr_max/weight_adapters.py:121-292, the MoE part).
+"""Checkpoint tensors -> one MoE layer's served weights (the MoE part of unlimited_ocr_max/weight_adapters.py).
 
-The reference's checkpoints hold every routed expert as its own tensor and the
-projections un-blocked; :class:`~uocr_moe.moe.MoE` takes the served layout.
-This module maps one ``model.layers.{L}.mlp`` from the first to the second:
+A checkpoint in the reference's layout holds every routed expert projection as
+its own ``[N, K]`` tensor, and the shared-expert projections un-blocked.
+:class:`~uocr_moe.moe.MoE` takes the served layout instead:
 
-* ``…mlp.gate.weight`` ``[E, H]`` (bf16 on disk) -> ``gate.gate_score.weight``
-  fp32, the router the reference serves in fp32 (decoder.py:19-22,227-229);
-* ``…mlp.experts.{j}.{gate,up,down}_proj.weight`` ``[N, K]`` -> one
-  ``experts.<proj>`` stack ``[E, N, K]`` in ascending expert index
-  (weight_adapters.py:121-166), int8 or bf16 as stored;
-* ``…weight_scales`` fp32 ``[N, K / 128]`` next to int8 weights ->
-  ``experts.<proj>_scales`` ``[E, N, K / 128]`` (the int8 form);
-* ``…mlp.shared_experts.<proj>.weight`` bf16 ``[N, K]`` -> K-blocked
-  ``[K / 16, N, 16]`` (weight_adapters.py:222-233).
+==========================================================  ==========================================
+checkpoint (``model.`` prefix optional)                     served (:class:`MoE` names)
+==========================================================  ==========================================
+``layers.L.mlp.gate.weight`` ``[E, H]`` (bf16 on disk)      ``gate.gate_score.weight`` fp32
+``layers.L.mlp.experts.j.<proj>.weight`` ``[N, K]``         ``experts.<proj>`` ``[E, N, K]``, j ascending
+``layers.L.mlp.experts.j.<proj>.weight_scales``             ``experts.<proj>_scales`` ``[E, N, K/G]`` fp32
+``layers.L.mlp.shared_experts.<proj>.weight`` ``[N, K]``    K-blocked ``[K/16, N, 16]`` bf16
+==========================================================  ==========================================
 
-The checks are the reference's: expert indices ``0..n-1`` with no gaps and
-exactly ``num_experts`` of them, one dtype and one shape per stack, and a
-half-quantized file (scales for some experts but not all, int8 weights with no
-scales, scales next to non-int8 weights) is an error, never a guess
-(weight_adapters.py:186-219).  Names with or without the ``model.`` prefix are
-accepted, as the reference matches both (weight_adapters.py:169-178).
+How it is read.  One pass over the checkpoint's names takes a census of the
+layer: a slot per (projection, expert index) holding that expert's weight and,
+on an int8 file, its scales.  Two ordered rule tables then judge the census;
+the first rule that finds offenders raises :class:`WeightMappingError` with its
+message, so a malformed file is refused for one named reason, never read as a
+guess:
+
+* the form rules decide int8 vs bf16 and refuse a half-quantized file (int8
+  weights without scales, scales without a weight, scales next to non-int8
+  weights, weights without scales while others have them) --
+  weight_adapters.py:186-219 states the same four refusals;
+* the stack rules check each of the six stacks (three projections, weights and
+  scales): expert indices 0..n-1 without gaps, exactly ``num_experts`` of them,
+  one dtype and one shape -- weight_adapters.py:121-163.
+
+The refusal texts are the reference's (its tests match them:
+tests/test_weight_adapters.py:124-222), and so is their order of precedence.
 """
 
 from __future__ import annotations
 
-import re
-from collections.abc import Mapping
+from collections.abc import Callable, Mapping
+from dataclasses import dataclass
 from pathlib import Path
 
 import torch
@@ -34,11 +44,6 @@ from .moe import ROUTED, MoE, MoeConfig
 from .ops import kblocked
 
 __all__ = ["WeightMappingError", "is_int8_checkpoint", "load_safetensors", "moe_from_checkpoint", "moe_layer_weights"]
-
-_EXPERT_RE = re.compile(
-    r"^(?:model\.)?layers\.(?P<layer>\d+)\.mlp\.experts\.(?P<expert>\d+)\."
-    r"(?P<proj>gate_proj|up_proj|down_proj)\.weight(?P<scales>_scales)?$"
-)
 
 
 class WeightMappingError(RuntimeError):
@@ -52,90 +57,150 @@ def load_safetensors(path: str | Path) -> dict[str, torch.Tensor]:
     return load_file(str(path), device="cpu")
 
 
-def _expert_tensors(checkpoint: Mapping[str, torch.Tensor], layer: int | None = None):
-    """``(weights, scales)`` keyed by ``(layer, expert, proj)``."""
-    weights: dict[tuple[int, int, str], torch.Tensor] = {}
-    scales: dict[tuple[int, int, str], torch.Tensor] = {}
-    for name, value in checkpoint.items():
-        m = _EXPERT_RE.match(name)
-        if m is None or (layer is not None and int(m["layer"]) != layer):
-            continue
-        key = (int(m["layer"]), int(m["expert"]), m["proj"])
-        (scales if m["scales"] else weights)[key] = value
-    return weights, scales
+# ----------------------------------------------------------------------------- the census
 
 
-def _names(keys, suffix: str = "") -> list[str]:
-    return [f"model.layers.{l}.mlp.experts.{e}.{p}.weight{suffix}" for l, e, p in sorted(keys)[:20]]
+def _routed_part(name: str) -> tuple[int, int, str, bool] | None:
+    """``(layer, expert, proj, is_scales)`` of a routed-expert tensor name, else None."""
+    parts = name.split(".")
+    if parts and parts[0] == "model":
+        parts = parts[1:]
+    if len(parts) != 7 or parts[0] != "layers" or parts[2:4] != ["mlp", "experts"]:
+        return None
+    layer, expert, proj, leaf = parts[1], parts[4], parts[5], parts[6]
+    if not (layer.isdigit() and expert.isdigit()) or proj not in ROUTED or leaf not in ("weight", "weight_scales"):
+        return None
+    return int(layer), int(expert), proj, leaf == "weight_scales"
+
+
+@dataclass
+class _Slot:
+    """One expert's projection: its weight and (int8 form) its scales, as found."""
+
+    weight: torch.Tensor | None = None
+    scales: torch.Tensor | None = None
+
+
+class _Census:
+    """Every routed-expert tensor of one layer (or of all layers: ``layer=None``), in one pass."""
+
+    def __init__(self, checkpoint: Mapping[str, torch.Tensor], layer: int | None) -> None:
+        self.slots: dict[tuple[int, int, str], _Slot] = {}
+        for name, value in checkpoint.items():
+            part = _routed_part(name)
+            if part is None or (layer is not None and part[0] != layer):
+                continue
+            slot = self.slots.setdefault(part[:3], _Slot())
+            if part[3]:
+                slot.scales = value
+            else:
+                slot.weight = value
+
+    def keys(self, pick: Callable[[_Slot], bool]) -> list[tuple[int, int, str]]:
+        return sorted(k for k, s in self.slots.items() if pick(s))
+
+    @property
+    def any_scales(self) -> bool:
+        return any(s.scales is not None for s in self.slots.values())
+
+
+def _listed(keys: list[tuple[int, int, str]], suffix: str = "") -> list[str]:
+    """At most 20 offenders, named as the checkpoint names them."""
+    return [f"model.layers.{l}.mlp.experts.{e}.{p}.weight{suffix}" for l, e, p in keys[:20]]
+
+
+def _dtype(t: torch.Tensor) -> str:
+    return str(t.dtype).removeprefix("torch.")
+
+
+def _is_int8(s: _Slot) -> bool:
+    return s.weight is not None and s.weight.dtype == torch.int8
+
+
+# The form rules, in order: (offenders of a census, message); the census is int8
+# when it has scales and no rule fires, bf16 when it has none.
+_FORM_RULES: tuple[tuple[Callable[[_Census], list], Callable[[_Census, list], str]], ...] = (
+    (lambda c: [] if c.any_scales else c.keys(_is_int8),
+     lambda c, ks: f"int8 expert weights without weight_scales: {_listed(ks)}"),
+    (lambda c: c.keys(lambda s: s.scales is not None and s.weight is None) if c.any_scales else [],
+     lambda c, ks: f"weight_scales without an expert weight to scale: {_listed(ks, '_scales')}"),
+    (lambda c: c.keys(lambda s: s.weight is not None and not _is_int8(s)) if c.any_scales else [],
+     lambda c, ks: "weight_scales are present but these expert weights are "
+                   f"{sorted({_dtype(c.slots[k].weight) for k in ks})}, not int8: {_listed(ks)}"),
+    (lambda c: c.keys(lambda s: s.weight is not None and s.scales is None) if c.any_scales else [],
+     lambda c, ks: f"half-quantized checkpoint: no weight_scales for {_listed(ks)}"),
+)
+
+
+def _judge_form(census: _Census) -> bool:
+    for offenders, message in _FORM_RULES:
+        found = offenders(census)
+        if found:
+            raise WeightMappingError(message(census, found))
+    return census.any_scales
 
 
 def is_int8_checkpoint(checkpoint: Mapping[str, torch.Tensor], layer: int | None = None) -> bool:
-    """Whether the routed experts are int8 with per-group ``weight_scales`` (False for the bf16 form)."""
-    weights, scales = _expert_tensors(checkpoint, layer)
-    quantized = {k for k, v in weights.items() if v.dtype == torch.int8}
-    if not scales:
-        if quantized:
-            raise WeightMappingError(f"int8 expert weights without weight_scales: {_names(quantized)}")
-        return False
-    orphans = set(scales) - set(weights)
-    if orphans:
-        raise WeightMappingError(f"weight_scales without an expert weight to scale: {_names(orphans, '_scales')}")
-    unquantized = set(weights) - quantized
-    if unquantized:
-        found = sorted({str(weights[k].dtype).removeprefix("torch.") for k in unquantized})
-        raise WeightMappingError(
-            f"weight_scales are present but these expert weights are {found}, not int8: {_names(unquantized)}")
-    bare = set(weights) - set(scales)
-    if bare:
-        raise WeightMappingError(f"half-quantized checkpoint: no weight_scales for {_names(bare)}")
-    return True
+    """Whether the routed experts are int8 with per-group ``weight_scales`` (False for the bf16 form);
+    a half-quantized file raises :class:`WeightMappingError`."""
+    return _judge_form(_Census(checkpoint, layer))
 
 
-def _stack(stacked: str, members: dict[int, torch.Tensor], num_experts: int) -> torch.Tensor:
-    """``members`` (expert index -> tensor) as one tensor in ascending index, with the reference's checks."""
-    indices = sorted(members)
-    if indices != list(range(len(indices))):
-        raise WeightMappingError(f"{stacked}: expert indices must be 0..n-1 with no gaps, got {indices}")
-    if len(indices) != num_experts:
-        raise WeightMappingError(f"{stacked}: expected {num_experts} experts, got {len(indices)}")
-    dtypes = {members[j].dtype for j in indices}
-    if len(dtypes) != 1:
-        found = sorted(str(d).removeprefix("torch.") for d in dtypes)
-        raise WeightMappingError(f"{stacked}: the experts disagree on dtype: {found}")
-    shapes = {tuple(members[j].shape) for j in indices}
-    if len(shapes) != 1:
-        raise WeightMappingError(f"{stacked}: the experts disagree on shape: {sorted(shapes)}")
-    return torch.stack([members[j] for j in indices]).contiguous()
+# ----------------------------------------------------------------------------- the stacks
 
 
-def _tensor(checkpoint: Mapping[str, torch.Tensor], layer: int, suffix: str) -> torch.Tensor:
-    for name in (f"model.layers.{layer}.mlp.{suffix}", f"layers.{layer}.mlp.{suffix}"):
-        if name in checkpoint:
-            return checkpoint[name]
-    raise WeightMappingError(f"model.layers.{layer}.mlp.{suffix}: not in the checkpoint")
+# The stack rules, in order, over ``members`` (expert index -> tensor): a failing
+# predicate raises with the message, prefixed by the stack's name.
+_STACK_RULES: tuple[tuple[Callable[[dict, int], bool], Callable[[dict, int], str]], ...] = (
+    (lambda m, n: sorted(m) == list(range(len(m))),
+     lambda m, n: f"expert indices must be 0..n-1 with no gaps, got {sorted(m)}"),
+    (lambda m, n: len(m) == n,
+     lambda m, n: f"expected {n} experts, got {len(m)}"),
+    (lambda m, n: len({t.dtype for t in m.values()}) == 1,
+     lambda m, n: f"the experts disagree on dtype: {sorted({_dtype(t) for t in m.values()})}"),
+    (lambda m, n: len({tuple(t.shape) for t in m.values()}) == 1,
+     lambda m, n: f"the experts disagree on shape: {sorted({tuple(t.shape) for t in m.values()})}"),
+)
+
+
+def _stacked(name: str, members: dict[int, torch.Tensor], num_experts: int) -> torch.Tensor:
+    for holds, message in _STACK_RULES:
+        if not holds(members, num_experts):
+            raise WeightMappingError(f"{name}: {message(members, num_experts)}")
+    return torch.stack([members[j] for j in range(num_experts)]).contiguous()
+
+
+def _mlp_tensor(checkpoint: Mapping[str, torch.Tensor], layer: int, leaf: str) -> torch.Tensor:
+    for prefix in ("model.", ""):
+        t = checkpoint.get(f"{prefix}layers.{layer}.mlp.{leaf}")
+        if t is not None:
+            return t
+    raise WeightMappingError(f"model.layers.{layer}.mlp.{leaf}: not in the checkpoint")
 
 
 def moe_layer_weights(checkpoint: Mapping[str, torch.Tensor], layer: int, *,
                       num_experts: int) -> tuple[dict[str, torch.Tensor], bool]:
     """Layer ``layer``'s MoE tensors under :class:`MoE`'s names, and whether its experts are int8."""
-    int8 = is_int8_checkpoint(checkpoint, layer)
-    weights, scales = _expert_tensors(checkpoint, layer)
-    if not weights:
+    census = _Census(checkpoint, layer)
+    int8 = _judge_form(census)
+    if not census.slots:
         raise WeightMappingError(f"model.layers.{layer}.mlp.experts: no expert weights in the checkpoint")
-    out: dict[str, torch.Tensor] = {"gate.gate_score.weight": _tensor(checkpoint, layer, "gate.weight").float()}
+    served: dict[str, torch.Tensor] = {"gate.gate_score.weight": _mlp_tensor(checkpoint, layer, "gate.weight").float()}
+    parts = ("weight", "scales") if int8 else ("weight",)
     for proj in ROUTED:
-        stacked = f"layers.{layer}.mlp.experts.{proj}"
-        out[f"experts.{proj}"] = _stack(stacked, {e: v for (_, e, p), v in weights.items() if p == proj}, num_experts)
-        if int8:
-            out[f"experts.{proj}_scales"] = _stack(
-                stacked + "_scales", {e: v for (_, e, p), v in scales.items() if p == proj}, num_experts).float()
+        for part in parts:
+            members = {e: getattr(s, part) for (_, e, p), s in census.slots.items()
+                       if p == proj and getattr(s, part) is not None}
+            suffix = "_scales" if part == "scales" else ""
+            stack = _stacked(f"layers.{layer}.mlp.experts.{proj}{suffix}", members, num_experts)
+            served[f"experts.{proj}{suffix}"] = stack.float() if part == "scales" else stack
     for proj in ROUTED:
-        w = _tensor(checkpoint, layer, f"shared_experts.{proj}.weight")
+        w = _mlp_tensor(checkpoint, layer, f"shared_experts.{proj}.weight")
         if w.dim() != 2:
             raise WeightMappingError(f"model.layers.{layer}.mlp.shared_experts.{proj}.weight: expected [N, K], "
                                      f"got shape {tuple(w.shape)}")
-        out[f"shared_experts.{proj}.weight"] = kblocked(w.to(torch.bfloat16))
-    return out, int8
+        served[f"shared_experts.{proj}.weight"] = kblocked(w.to(torch.bfloat16))
+    return served, int8
 
 
 def moe_from_checkpoint(checkpoint: Mapping[str, torch.Tensor], layer: int, *, num_experts: int = 64,
