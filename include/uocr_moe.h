@@ -264,6 +264,25 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
                          const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
                          void* workspace, size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
+/* uocr_moe_decode_rows_static -- uocr_moe_decode_rows without any allocation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, bits and routing outputs as
+ * uocr_moe_decode_rows, minus the workspace: its scratch is one static 16 MiB
+ * device array per GPU (9 MiB for the persistent kernel's control words and
+ * tagged arena, 7 MiB of multi-kernel workspace), resolved and cleared by the
+ * first call on each device and held until the process ends.  It calls no
+ * hipMalloc or hipFree.  A call whose layer and row count need more than the
+ * 7 MiB (only the multi-kernel path can: rows > 8, or a layer the persistent
+ * kernel does not take) is refused before anything is enqueued.  Every call on
+ * a GPU shares that GPU's array: calls that overlap in time on one GPU (other
+ * streams, other threads) race and must not be made.  A persistent launch whose
+ * bounded waits ran out poisons the array's arena (NaN outputs) until
+ * uocr_moe_fused_errors on any stream of that device reports and clears it. */
+int uocr_moe_decode_rows_static(float* out, const float* x, int64_t rows, int64_t hidden,
+                                const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
+                                void* stream, char* err, size_t errlen);
+
 /* MoE.__call__ (prefill) -- replaces unlimited_ocr_max/decoder.py:657-667
  * (the dense 64-expert chain of the int8 path, _routed_native of the bf16
  * path).  x fp32 [T, H] -> out fp32 [T, H].  The top-k experts of every token
@@ -278,8 +297,8 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden,
  * control words.  No call may be in flight. */
 void uocr_moe_release(void);
 
-/* Waits for `stream` and reports whether a persistent decode launch on it ran
- * out of its bounded waits: errors = 1.
+/* Waits for `stream` and reports whether a persistent decode launch on it (or
+ * on the device's static scratch) ran out of its bounded waits: errors = 1.
  * Such a launch wrote NaN where its outputs depended on what it waited for,
  * and every later launch on the same slot writes NaN until this call, which
  * then clears the slot (control words and tagged arena).  The waits run out

@@ -185,3 +185,15 @@ def test_quantize_refusals() -> None:
         "quantize_per_group: K=100 is not divisible by the group size 128"
     assert "bad group size" in _err("uocr_quantize_per_group", 8, 8, 8, 0, 2, 128, 0, None)
 
+
+def test_static_decode_refuses_beyond_its_scratch() -> None:
+    """The allocation-free decode refuses, before any device call, a call whose multi-kernel workspace would
+    not fit its static scratch (64 rows of a layer 2048 wide)."""
+    from uocr_moe import _lib
+
+    fake = 4096  # never dereferenced: the call is refused on the host
+    layer = _lib.Layer(64, 2048, 2048, 2048, 6, 128, 0, 0, fake, fake, fake, fake, None, None, None, fake, fake, fake)
+    msg = _err("uocr_moe_decode_rows_static", None, None, 64, 2048, ctypes.byref(layer), None, None, None)
+    assert msg.startswith("uocr_moe_decode_rows_static: 64 rows of this layer need ") and "more than the" in msg
+    msg = _err("uocr_moe_decode_rows_static", None, None, 65, 2048, ctypes.byref(layer), None, None, None)
+    assert msg == "uocr_moe_decode_rows_static: rows must be in [0, 64]"

@@ -21,6 +21,16 @@ namespace uocr {
 int gemm_bk();
 }  // namespace uocr
 
+// Scratch of the allocation-free decode entry (uocr_moe_decode_rows_static): one
+// array per GPU, held until the process ends.  The first kScratchFusedBytes
+// hold the persistent kernel's control words and tagged arena (room for any
+// layer the persistent path accepts); the rest is the multi-kernel decode's
+// workspace.  Host code never passes `scratch` itself to a kernel: it passes
+// the device address hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+constexpr size_t kScratchFusedBytes = (size_t)9 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 using namespace uocr;
 
 // ------------------------------------------------------------------ kernel timing
@@ -136,6 +146,7 @@ struct FusedDevice {
 };
 std::map<int, FusedDevice> g_fused;
 std::map<std::pair<int, size_t>, int> g_fused_grid;  // (device, LDS bytes) -> workgroups
+std::map<int, char*> g_scratch;  // device -> the address of `scratch` on it
 
 // Optional phase trace of the next persistent decode launch (diagnostics).
 int64_t* g_trace = nullptr;
@@ -879,8 +890,8 @@ int uocr_moe_gate(int64_t* indices, float* weights, const float* x, int64_t seq,
 
 }  // extern "C"
 
-// The decode layer.  fixed: the persistent kernel's control words and arena,
-// given by the caller; null: the stream's own slot.
+// The decode layer of both decode entry points.  fixed: the persistent kernel's
+// control words and arena (the static scratch's); null: the stream's own slot.
 static int decode_rows_impl(const char* op, float* out, const float* x, int64_t rows, int64_t hidden,
                             const uocr_moe_layer* L, int32_t* expert_ids, float* expert_weights, void* workspace,
                             size_t workspace_bytes, hipStream_t s, const FusedSlot* fixed, char* err,
@@ -1026,6 +1037,31 @@ static int decode_rows_impl(const char* op, float* out, const float* x, int64_t 
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
 
+// The address of `scratch` on the current device, looked up once per device;
+// that first call also clears the persistent kernel's region with a kernel (the
+// array is zero at load; a kernel rather than a memset because this call may
+// be under stream capture).
+static hipError_t scratch_base(hipStream_t s, char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  auto it = g_scratch.find(dev);
+  if (it != g_scratch.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (p == nullptr) return hipErrorInvalidSymbol;
+  e = launch_zero_words(static_cast<uint32_t*>(p), (int64_t)(kScratchFusedBytes / 4), s);
+  if (e != hipSuccess) return e;
+  g_scratch[dev] = static_cast<char*>(p);
+  *out = static_cast<char*>(p);
+  return hipSuccess;
+}
+
 extern "C" {
 
 int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidden, const uocr_moe_layer* L,
@@ -1033,6 +1069,31 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
                          void* stream, char* err, size_t errlen) {
   return decode_rows_impl("uocr_moe_decode_rows", out, x, rows, hidden, L, expert_ids, expert_weights, workspace,
                           workspace_bytes, (hipStream_t)stream, nullptr, err, errlen);
+}
+
+int uocr_moe_decode_rows_static(float* out, const float* x, int64_t rows, int64_t hidden, const uocr_moe_layer* L,
+                                int32_t* expert_ids, float* expert_weights, void* stream, char* err, size_t errlen) {
+  const char* op = "uocr_moe_decode_rows_static";
+  // every size check runs before the first device call
+  if (check_layer(op, L, hidden, err, errlen)) return 1;
+  if (rows < 0 || rows > 64) return fail(err, errlen, "%s: rows must be in [0, 64]", op);
+  if (rows == 0) return 0;
+  if ((size_t)kFusedCtlWords * 4 + (size_t)fused_max_words() * 8 > kScratchFusedBytes)
+    return fail(err, errlen, "%s: the persistent kernel's arena does not fit the scratch", op);
+  if (!fused_eligible(L, rows)) {
+    Carve dry(nullptr);
+    carve_decode(dry, L, rows);
+    if (dry.off > kScratchBytes - kScratchFusedBytes)
+      return fail(err, errlen, "%s: %lld rows of this layer need %zu bytes of scratch, more than the %zu it has", op,
+                  (long long)rows, dry.off, kScratchBytes - kScratchFusedBytes);
+  }
+  const hipStream_t s = (hipStream_t)stream;
+  char* base = nullptr;
+  const hipError_t e = scratch_base(s, &base);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+  const FusedSlot fixed{reinterpret_cast<uint32_t*>(base), reinterpret_cast<uint64_t*>(base + (size_t)kFusedCtlWords * 4)};
+  return decode_rows_impl(op, out, x, rows, hidden, L, expert_ids, expert_weights, base + kScratchFusedBytes,
+                          kScratchBytes - kScratchFusedBytes, s, &fixed, err, errlen);
 }
 
 int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, const uocr_moe_layer* L,
@@ -1204,7 +1265,7 @@ int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errl
   const hipStream_t s = (hipStream_t)stream;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  // the stream's slot (control words, then the tagged arena)
+  // the stream's slot and the device's static scratch (each: control words, then the tagged arena)
   std::vector<std::pair<uint32_t*, int64_t>> areas;
   if (e == hipSuccess) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
@@ -1213,6 +1274,8 @@ int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errl
       auto sl = it->second.slot.find(s);
       if (sl != it->second.slot.end()) areas.emplace_back(sl->second.ctl, (int64_t)(fused_slot_bytes() / 4));
     }
+    auto sc = g_scratch.find(dev);
+    if (sc != g_scratch.end()) areas.emplace_back(reinterpret_cast<uint32_t*>(sc->second), (int64_t)(kScratchFusedBytes / 4));
   }
   uint32_t v[2] = {0u, 0u};
   for (size_t i = 0; e == hipSuccess && i < areas.size(); ++i)
