@@ -31,6 +31,7 @@ import os
 import statistics
 import sys
 import time
+from collections.abc import Callable
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -47,6 +48,8 @@ FS = N_SHARED * F
 LAYERS = 11
 ZIPF_S = 1.1
 ZIPF_SCALE = 0.75
+PREFILL_4K_LAYERS = 4
+XCDS, SIMDS = 8, 1024  # MI355X: 8 XCDs, 256 CUs x 4 SIMDs
 
 
 def log(msg: str) -> None:
@@ -162,7 +165,48 @@ def kernel_times(fn_steps) -> dict[str, list[float]]:
     return out
 
 
+def fused_errors() -> int:
+    """The persistent decode kernel's error word after everything queued so far (0: every bounded wait
+    ended in time, so the timed launches computed real outputs)."""
+    from uocr_moe import _lib
+
+    return _lib.fused_errors()
+
+
 # ---------------------------------------------------------------------------- benchmark parts
+
+
+def bench_stack(layers, B: int, steps: int, device: str, seed: int) -> dict:
+    """The MoE stack of one decode step: the 11 int8 layers chained through the residual stream,
+    x_{l+1} = x_l + MoE_l(x_l) as the decoder's layers add it (so routing differs per layer and the batch's
+    tokens stay distinct), ``steps // 11`` whole steps in one graph.  The step time includes the 11
+    residual adds (one small elementwise kernel each)."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    x0 = rmsnorm_rows(g, B, device)
+    ws = layers[0].workspace(B, prefill=False)
+    u, x = [], x0
+    for moe in layers:
+        y, ids, _ = moe.decode_rows(x, workspace=ws, routing=True)
+        x = x + y
+        u.append(int(torch.unique(ids).numel()))
+
+    def step():
+        y = x0
+        for moe in layers:
+            y = y + moe.decode_rows(y, workspace=ws)
+
+    nsteps = max(1, steps // LAYERS)
+    ms = time_graph(graph_of([step] * nsteps))
+    errors = fused_errors()
+    us = ms * 1e3 / nsteps
+    nbytes = sum(decode_bytes(ui, B, True) for ui in u)
+    return {"rows": B, "layers": LAYERS, "us_per_step": round(us, 2), "tokens_per_s": round(B / (us * 1e-6), 1),
+            "steps_in_graph": nsteps, "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "distinct_experts": u,
+            "fused_errors": errors,
+            "chain": "x_{l+1} = x_l + MoE_l(x_l) over the 11 layers (residual adds included), measured"}
 
 
 def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: str, seed: int) -> dict:
@@ -183,12 +227,14 @@ def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: st
         graph_of(wfns).replay()
     graph = graph_of(fns)
     ms = time_graph(graph)
+    errors = fused_errors()
     us = ms * 1e3 / steps
     total_bytes = sum(decode_bytes(u_of[p], B, int8) for _, p in plan)
     gbs = total_bytes / (ms * 1e-3) / 1e9
     # warm: one layer, one batch, repeated
     wgraph = graph_of([lambda: layers[0].decode_rows(pool[0], workspace=ws)] * min(steps, 4 * LAYERS))
     warm_us = time_graph(wgraph) * 1e3 / min(steps, 4 * LAYERS)
+    errors += fused_errors()
     warm_gbs = decode_bytes(u_of[0], B, int8) / (warm_us * 1e-6) / 1e9
     # live per-kernel durations over one rotation (eager; events around each launch)
     kt = kernel_times([lambda l=l, p=p: layers[l].decode_rows(pool[p], workspace=ws) for l, p in plan[: 4 * LAYERS]])
@@ -205,6 +251,7 @@ def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: st
         "warm_gbs": round(warm_gbs, 1),
         "kernels_us_avg": {k: round(1e3 * statistics.mean(v), 3) for k, v in kt.items()},
         "kernel_sum_us_avg": round(1e3 * sum(sum(v) for v in kt.values()) / (4 * LAYERS), 3),
+        "fused_errors": errors + fused_errors(),
     }
     if fused:
         res["fused_kernel"] = {
@@ -385,7 +432,9 @@ def zipf_prefill_inputs(g, T: int, device: str, seed: int):
     return x.contiguous(), bias
 
 
-def bench_prefill(layers_w, T: int, device: str, seed: int, adversarial: bool = False) -> dict:
+def prefill_setup(layers_w, T: int, device: str, seed: int, adversarial: bool = False):
+    """``(moes, x, workspace)``: the layers with the Zipf bias (or the adversarial +10 on experts 0-5) in their
+    router's column 0, and the T input rows whose constant feature carries it."""
     import torch
     import uocr_moe
 
@@ -399,7 +448,13 @@ def bench_prefill(layers_w, T: int, device: str, seed: int, adversarial: bool = 
         r = w["gate.gate_score.weight"].clone()
         r[:, 0] = bias
         moes.append(uocr_moe.MoE(moe.config, {**w, "gate.gate_score.weight": r}))
-    ws = moes[0].workspace(T, prefill=True)
+    return moes, x, moes[0].workspace(T, prefill=True)
+
+
+def bench_prefill(layers_w, T: int, device: str, seed: int, adversarial: bool = False) -> dict:
+    import torch
+
+    moes, x, ws = prefill_setup(layers_w, T, device, seed, adversarial)
     hist = None
     touched = []
     for m in moes:
@@ -435,8 +490,24 @@ def bench_prefill(layers_w, T: int, device: str, seed: int, adversarial: bool = 
     }
 
 
-def bench_cpu_baseline(layer_w, budget_s: float) -> dict:
-    """The reference's CPU decomposition (the oracle's restatement) on this host: int8 layer, B=1 and B=8."""
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu), for the baseline record."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+    for line in out.splitlines():
+        if line.startswith("Model name:"):
+            return line.split(":", 1)[1].strip()
+    return "unknown"
+
+
+def bench_cpu_baseline(layer_int8, layer_bf16, budget_s: float, min_runs: int = 20) -> dict:
+    """The reference's CPU decomposition (the oracle's restatement of the CPU path) on this host: the int8
+    layer and its bf16 source layer, B=1 and B=8, on every host core and on one, medians of at least
+    ``min_runs`` runs after a warm-up (about ``budget_s`` seconds in all)."""
     import numpy as np
     import torch
 
@@ -447,26 +518,34 @@ def bench_cpu_baseline(layer_w, budget_s: float) -> dict:
             return t.view(torch.int16).cpu().numpy().view(np.uint16)
         return t.cpu().numpy()
 
-    w = {k: host(v) for k, v in layer_w.items()}
-    layer = O.MoeWeights(router=w["gate.gate_score.weight"], gate=w["experts.gate_proj"], up=w["experts.up_proj"],
-                         down=w["experts.down_proj"], gate_s=w["experts.gate_proj_scales"],
-                         up_s=w["experts.up_proj_scales"], down_s=w["experts.down_proj_scales"],
-                         sh_gate=w["shared_experts.gate_proj.weight"], sh_up=w["shared_experts.up_proj.weight"],
-                         sh_down=w["shared_experts.down_proj.weight"], topk=TOPK, group=GROUP)
+    def weights(w):
+        w = {k: host(v) for k, v in w.items()}
+        kw = dict(router=w["gate.gate_score.weight"], gate=w["experts.gate_proj"], up=w["experts.up_proj"],
+                  down=w["experts.down_proj"], sh_gate=w["shared_experts.gate_proj.weight"],
+                  sh_up=w["shared_experts.up_proj.weight"], sh_down=w["shared_experts.down_proj.weight"], topk=TOPK,
+                  group=GROUP)
+        if "experts.gate_proj_scales" in w:
+            kw.update(gate_s=w["experts.gate_proj_scales"], up_s=w["experts.up_proj_scales"],
+                      down_s=w["experts.down_proj_scales"])
+        return O.MoeWeights(**kw)
+
     rng = np.random.default_rng(5)
     cores = O.threads(0)
-    out = {"cores": cores}
-    for B in (1, 8):
+    out = {"cores": cores, "model": cpu_model()}
+    cases = [(kind, layer, B, t) for kind, layer in (("int8", weights(layer_int8)), ("bf16", weights(layer_bf16)))
+             for B in (1, 8) for t in (cores, 1)]
+    per_case = budget_s / len(cases)
+    for kind, layer, B, threads in cases:
         x = O.rmsnorm_rows(rng, B, H)
-        O.moe_decode_refdecomp(x, layer, threads=cores)  # warm-up
+        O.moe_decode_refdecomp(x, layer, threads=threads)  # warm-up
         times = []
-        t_end = time.perf_counter() + budget_s / 2
-        while time.perf_counter() < t_end or len(times) < 3:
+        t_end = time.perf_counter() + per_case
+        while time.perf_counter() < t_end or len(times) < min_runs:
             t0 = time.perf_counter()
-            O.moe_decode_refdecomp(x, layer, threads=cores)
+            O.moe_decode_refdecomp(x, layer, threads=threads)
             times.append(time.perf_counter() - t0)
-        out[f"b{B}_us"] = round(1e6 * statistics.median(times), 1)
-        out[f"b{B}_runs"] = len(times)
+        key = f"{kind}_b{B}_{'all' if threads == cores else '1core'}"
+        out[key] = {"us": round(1e6 * statistics.median(times), 1), "runs": len(times), "threads": threads}
     return out
 
 
@@ -496,9 +575,9 @@ def traffic_probe() -> int:
     return 0
 
 
-def measure_traffic(kernel: str, timeout_s: int = 120) -> dict | None:
-    """HBM bytes per launch of ``kernel`` from two ``rocprofv3 --pmc`` passes (FETCH_SIZE, WRITE_SIZE) over
-    ``--traffic-probe``, each scaled so that the elementwise kernel reads and writes its known 256 MiB."""
+def run_counters(probe: str, counters: list[str], timeout_s: int = 150) -> list[tuple[int, str, dict]] | None:
+    """One ``rocprofv3 --pmc`` pass over ``bench.py <probe>`` (a child process): per dispatch, in dispatch
+    order, ``(dispatch id, kernel name, {counter: value summed over its instances})``."""
     import csv
     import shutil
     import subprocess
@@ -506,37 +585,125 @@ def measure_traffic(kernel: str, timeout_s: int = 120) -> dict | None:
 
     prof = shutil.which("rocprofv3")
     if prof is None:
-        log("traffic: rocprofv3 not found")
+        log("counters: rocprofv3 not found")
         return None
-    res: dict = {}
     with tempfile.TemporaryDirectory(dir="/tmp") as d:
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", counter, "--output-format", "csv",
-                   "-d", d, "-o", counter, "--", sys.executable, str(ROOT / "bench.py"), "--traffic-probe"]
-            log(f"traffic: {counter} pass")
-            r = subprocess.run(cmd, capture_output=True, text=True, env={**os.environ, "TMPDIR": "/tmp"})
-            if r.returncode != 0:
-                log(f"traffic: {counter} pass failed ({r.returncode}): {r.stderr[-400:]}")
+        cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", *counters, "--output-format", "csv", "-d", d,
+               "-o", "pmc", "--", sys.executable, str(ROOT / "bench.py"), probe]
+        log(f"counters: {' '.join(counters)} over {probe}")
+        r = subprocess.run(cmd, capture_output=True, text=True, env={**os.environ, "TMPDIR": "/tmp"})
+        path = Path(d) / "pmc_counter_collection.csv"
+        if r.returncode != 0 and not path.exists():
+            log(f"counters: pass failed ({r.returncode}): {r.stderr[-400:]}")
+            return None
+        per: dict[tuple[int, str], dict] = {}
+        for row in csv.DictReader(open(path)):
+            key = (int(row["Dispatch_Id"]), row["Kernel_Name"])
+            c = per.setdefault(key, {})
+            c[row["Counter_Name"]] = c.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    return [(k[0], k[1], v) for k, v in sorted(per.items())]
+
+
+def measure_traffic(probe: str, kernels: dict[str, Callable[[list], list]]) -> dict | None:
+    """HBM bytes per launch from two passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled so
+    that the probe's closing elementwise kernel reads and writes its known 256 MiB.  ``kernels`` maps a
+    label to a selector of that label's dispatches from the list of (id, name, counters)."""
+    res: dict = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = run_counters(probe, [counter])
+        if rows is None:
+            return None
+        scale = [c[counter] for _, n, c in rows if "neg" in n]
+        if not scale:
+            log(f"traffic: {counter}: no dispatches of the scale kernel")
+            return None
+        factor = COPY_ELEMS * 4 / 1024 / statistics.mean(scale)
+        for label, pick in kernels.items():
+            mine = [c[counter] for _, _, c in pick(rows)]
+            if not mine:
+                log(f"traffic: {counter}: no dispatches of {label}")
                 return None
-            path = Path(d) / f"{counter}_counter_collection.csv"
-            per: dict[tuple[str, str], float] = {}
-            for row in csv.DictReader(open(path)):
-                if row["Counter_Name"] != counter:
-                    continue
-                key = (row["Dispatch_Id"], row["Kernel_Name"])
-                per[key] = per.get(key, 0.0) + float(row["Counter_Value"])
-            ours = [v for (_, n), v in per.items() if kernel in n]
-            scale = [v for (_, n), v in per.items() if "neg" in n]
-            if not ours or not scale:
-                log(f"traffic: {counter}: no dispatches of {kernel} or of the scale kernel")
-                return None
-            known_kib = COPY_ELEMS * 4 / 1024
-            factor = known_kib / statistics.mean(scale)
-            res[counter] = {"kib_per_launch": round(statistics.mean(ours), 1), "launches": len(ours),
-                            "scale_kernel_kib": round(statistics.mean(scale), 1), "factor": round(factor, 4)}
-    fetch = res["FETCH_SIZE"]["kib_per_launch"] * res["FETCH_SIZE"]["factor"] * 1024
-    write = res["WRITE_SIZE"]["kib_per_launch"] * res["WRITE_SIZE"]["factor"] * 1024
-    return {"bytes": int(fetch + write), "fetch_bytes": int(fetch), "write_bytes": int(write), "counters": res}
+            r = res.setdefault(label, {})
+            r[counter] = {"kib_per_launch": round(statistics.mean(mine), 1), "launches": len(mine),
+                          "scale_kernel_kib": round(statistics.mean(scale), 1), "factor": round(factor, 4)}
+    for label, r in res.items():
+        fetch = r["FETCH_SIZE"]["kib_per_launch"] * r["FETCH_SIZE"]["factor"] * 1024
+        write = r["WRITE_SIZE"]["kib_per_launch"] * r["WRITE_SIZE"]["factor"] * 1024
+        r.update({"bytes": int(fetch + write), "fetch_bytes": int(fetch), "write_bytes": int(write)})
+    return res
+
+
+def _by_name(part: str) -> Callable[[list], list]:
+    return lambda rows: [r for r in rows if part in r[1]]
+
+
+def prefill_gemm_dispatches(rows: list) -> dict[str, list]:
+    """The prefill probe's GEMM dispatches by workload, in its launch order: T=512 over the 11 layers, then
+    T=4096 and the adversarial T=4096 over 4 layers each; gate/up and down alternate within a layer."""
+    gemms = [r for r in rows if "k_gemm_pair" in r[1]]
+    n512, n4k = 2 * LAYERS, 2 * PREFILL_4K_LAYERS
+    groups = {"t512": gemms[:n512], "t4096": gemms[n512:n512 + n4k], "t4096_adversarial": gemms[n512 + n4k:]}
+    out = {}
+    for name, g in groups.items():
+        out[f"{name}_gateup"] = g[0::2]
+        out[f"{name}_down"] = g[1::2]
+    return out
+
+
+def prefill_probe() -> int:
+    """Child mode run under ``rocprofv3 --pmc``: the bench's prefill workloads (T=512 with Zipf routing over
+    the 11 layers, T=4096 and its adversarial case over 4), then the elementwise kernel that scales the
+    traffic counters."""
+    import torch
+
+    dev = "cuda:0"
+    layers_w = [make_layer(1000 + l, True, dev) for l in range(LAYERS)]
+    for T, n, seed, adv in ((512, LAYERS, 512, False), (4096, PREFILL_4K_LAYERS, 4096, False),
+                            (4096, PREFILL_4K_LAYERS, 4097, True)):
+        moes, x, ws = prefill_setup(layers_w[:n], T, dev, seed, adv)
+        for m in moes:
+            m(x, workspace=ws)
+        torch.cuda.synchronize()
+        del moes, ws
+    src = torch.ones(COPY_ELEMS, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("prefill probe done", flush=True)
+    return 0
+
+
+def measure_prefill_counters(results: dict) -> dict | None:
+    """MFMA utilisation and HBM traffic of the prefill GEMMs from rocprofv3 counters.
+
+    * ``mfma_busy_frac`` = SQ_VALU_MFMA_BUSY_CYCLES (summed over every SIMD) / (GRBM_GUI_ACTIVE per XCC x
+      1024 SIMDs): the fraction of the kernel's active cycles the matrix cores were busy.
+    * ``mfma_flops`` = 512 x SQ_INSTS_VALU_MFMA_MOPS_BF16: the FLOPs the matrix cores executed, padded rows
+      included (against the launch's algorithmic FLOPs).
+    * ``bytes`` (FETCH_SIZE + WRITE_SIZE, scaled by the copy kernel).
+    """
+    rows = run_counters("--prefill-probe", ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                                            "GRBM_GUI_ACTIVE"])
+    if rows is None:
+        return None
+    groups = prefill_gemm_dispatches(rows)
+    out: dict = {}
+    for label, disp in groups.items():
+        if not disp:
+            continue
+        busy = [c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] / XCDS * SIMDS) for _, _, c in disp]
+        flops = [512.0 * c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for _, _, c in disp]
+        out[label] = {"launches": len(disp), "mfma_busy_frac": round(statistics.mean(busy), 4),
+                      "mfma_flops_per_launch": round(statistics.mean(flops)),
+                      "active_cycles_per_xcd": round(statistics.mean(c["GRBM_GUI_ACTIVE"] / XCDS for _, _, c in disp))}
+    traffic = measure_traffic("--prefill-probe", {k: (lambda rows, k=k: prefill_gemm_dispatches(rows)[k])
+                                                  for k in groups})
+    if traffic is not None:
+        for label, t in traffic.items():
+            out.setdefault(label, {})["traffic_bytes"] = t["bytes"]
+            out[label]["traffic"] = {k: t[k] for k in ("FETCH_SIZE", "WRITE_SIZE")}
+    return out
 
 
 # ---------------------------------------------------------------------------- main
@@ -547,15 +714,19 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=440, help="timed decode layer-steps (one graph replay)")
     ap.add_argument("--warmup", type=int, default=44)
-    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline sampling")
+    ap.add_argument("--cpu-budget", type=float, default=16.0, help="seconds of CPU-baseline sampling")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="decode only (no prefill, no bf16)")
     ap.add_argument("--batches", default="1,8", help="int8 decode batches to time (1 is required)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc traffic passes")
+    ap.add_argument("--no-counters", action="store_true", help="skip the rocprofv3 --pmc passes over the prefill")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--prefill-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.traffic_probe:
         return traffic_probe()
+    if args.prefill_probe:
+        return prefill_probe()
     batches = sorted({int(b) for b in args.batches.split(",")})
     if 1 not in batches:
         print("--batches must include 1 (the headline workload)", file=sys.stderr)
@@ -589,14 +760,10 @@ def main() -> int:
         log(f"decode int8 B={B}")
         results[f"decode_int8_b{B}"] = bench_decode(layers, B, args.steps, args.warmup, True, dev, B)
         log(f"  {results[f'decode_int8_b{B}']['us_per_layer']} us/layer")
-    if 8 in batches:
-        # the B=8 graph is args.steps consecutive launches that walk the 11 layers in order
-        # (layer i % 11), i.e. args.steps / 11 whole decode steps of the MoE stack
-        us8 = results["decode_int8_b8"]["us_per_layer"]
-        results["decode_int8_11layer_step_b8"] = {
-            "us_per_step": round(LAYERS * us8, 2), "tokens_per_s": round(8 / (LAYERS * us8 * 1e-6), 1),
-            "steps_in_graph": args.steps // LAYERS, "layers": LAYERS,
-            "inputs": "an independent RMS-normalised batch per layer launch"}
+    for B in (1, 8):
+        log(f"decode int8, the 11-layer MoE stack chained, B={B}")
+        results[f"decode_int8_11layer_step_b{B}"] = bench_stack(layers, B, args.steps, dev, 11 + B)
+        log(f"  {results[f'decode_int8_11layer_step_b{B}']['us_per_step']} us/step")
     if not args.quick:
         for B in (1, 8):
             log(f"decode step, 12 layers + lm_head, B={B}")
@@ -606,13 +773,17 @@ def main() -> int:
         results["prefill_int8_t512"] = bench_prefill(layers_w, 512, dev, 512)
         log(f"  {results['prefill_int8_t512']['tflops']} TFLOP/s")
         log("prefill int8 T=4096")
-        results["prefill_int8_t4096"] = bench_prefill(layers_w[:4], 4096, dev, 4096)
-        results["prefill_int8_t4096_adversarial"] = bench_prefill(layers_w[:4], 4096, dev, 4097, adversarial=True)
+        results["prefill_int8_t4096"] = bench_prefill(layers_w[:PREFILL_4K_LAYERS], 4096, dev, 4096)
+        results["prefill_int8_t4096_adversarial"] = bench_prefill(layers_w[:PREFILL_4K_LAYERS], 4096, dev, 4097,
+                                                                  adversarial=True)
         log(f"  {results['prefill_int8_t4096']['tflops']} / {results['prefill_int8_t4096_adversarial']['tflops']} TFLOP/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        cpu = bench_cpu_baseline(layers_w[0][1], args.cpu_budget)
+        bf_src = make_layer(1000, False, dev)[1]  # the bf16 weights the first int8 layer was quantised from
+        cpu = bench_cpu_baseline(layers_w[0][1], bf_src, args.cpu_budget)
+        del bf_src
+        log(f"  {cpu}")
     if not args.quick:
         del layers_w, layers
         torch.cuda.empty_cache()
@@ -636,9 +807,30 @@ def main() -> int:
     fk = b1.get("fused_kernel", {})
     traffic = None
     if not args.no_traffic:
-        traffic = measure_traffic("k_decode_fused")
-        if traffic is not None:
+        t = measure_traffic("--traffic-probe", {"decode_fused": _by_name("k_decode_fused")})
+        if t is not None:
+            traffic = t["decode_fused"]
             results["traffic_decode_int8_b1"] = traffic
+    if not args.quick and not args.no_counters:
+        pc = measure_prefill_counters(results)
+        if pc is not None:
+            results["prefill_counters"] = pc
+            for key, label in (("prefill_int8_t512", "t512"), ("prefill_int8_t4096", "t4096"),
+                               ("prefill_int8_t4096_adversarial", "t4096_adversarial")):
+                r = results.get(key)
+                if r is None:
+                    continue
+                for kind, kname in (("gateup", "gemm_gateup"), ("down", "gemm_down")):
+                    c = pc.get(f"{label}_{kind}")
+                    us = r["kernels_us_avg"].get(kname)
+                    if c is None or us is None:
+                        continue
+                    c["kernel_us"] = us
+                    c["mfma_tflops_executed"] = round(c["mfma_flops_per_launch"] / (us * 1e-6) / 1e12, 1)
+                    if "traffic_bytes" in c:
+                        c["traffic_gbs"] = round(c["traffic_bytes"] / (us * 1e-6) / 1e9, 1)
+                r["mfma_busy_frac"] = {k: pc[f"{label}_{k}"]["mfma_busy_frac"] for k in ("gateup", "down")
+                                       if f"{label}_{k}" in pc}
     line = {
         "metric": METRIC,
         "value": b1["us_per_layer"],
@@ -668,14 +860,24 @@ def main() -> int:
             "avg_launch_us": fk.get("avg_us"),
         },
         "cpu_baseline": None if cpu is None else {
-            "value": cpu["b1_us"], "unit": "us", "cores": cpu["cores"], "kind": "port",
-            "sample": f"int8 decode layer B=1, median of {cpu['b1_runs']} runs (B=8: {cpu['b8_us']} us, "
-                      f"{cpu['b8_runs']} runs); the reference's CPU decomposition restated in C",
+            "value": cpu["int8_b1_all"]["us"], "unit": "us", "cores": cpu["cores"], "kind": "port",
+            "sample": f"int8 decode layer B=1 on all {cpu['cores']} host threads ({cpu['model']}), median of "
+                      f"{cpu['int8_b1_all']['runs']} runs; the reference's CPU decomposition restated in C. "
+                      f"1 core: {cpu['int8_b1_1core']['us']} us; B=8: {cpu['int8_b8_all']['us']} us all cores, "
+                      f"{cpu['int8_b8_1core']['us']} us 1 core; the bf16 layer (its unquantised source) B=1: "
+                      f"{cpu['bf16_b1_all']['us']} / {cpu['bf16_b1_1core']['us']} us, B=8: "
+                      f"{cpu['bf16_b8_all']['us']} / {cpu['bf16_b8_1core']['us']} us (all cores / 1 core)",
+            "model": cpu["model"],
+            "medians_us": {k: v for k, v in cpu.items() if k not in ("cores", "model")},
         },
         "results": results,
         "wall_s": round(time.perf_counter() - t_start, 1),
     }
     print(json.dumps(line), flush=True)
+    failed = [k for k, r in results.items() if isinstance(r, dict) and r.get("fused_errors")]
+    if failed:
+        log(f"the persistent decode kernel reported failed waits in {failed}: those timings are not valid")
+        return 1
     return 0
 
 
