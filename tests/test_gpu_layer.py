@@ -316,9 +316,10 @@ def test_unaligned_output_pointer(oracle, small) -> None:
 
 
 def test_decode_failure_is_loud_and_recoverable(oracle, small, monkeypatch) -> None:
-    """The persistent kernel's bounded waits, forced to run out from the host (a spin limit of one poll),
-    end the launch normally with NaN outputs and the error word set; later launches on the slot write NaN
-    until ``fused_errors`` reports and clears it; the next launch is bitwise the oracle again."""
+    """The persistent kernel's bounded waits, forced to fail from the host (a spin limit of 0: every wait
+    gives up at its first check), end the launch normally with NaN outputs and the error word set; later
+    launches on the slot write NaN until ``fused_errors`` reports and clears it; the next launch is bitwise
+    the oracle again."""
     from uocr_moe import _lib
 
     layer = small[True]
@@ -327,10 +328,10 @@ def test_decode_failure_is_loud_and_recoverable(oracle, small, monkeypatch) -> N
     want = oracle.moe_decode_exact(x, layer)[0]
     assert bits_equal(n(moe.decode_rows(t(x))), want)
     assert _lib.fused_errors() == 0
-    monkeypatch.setenv("UOCR_MOE_SPIN_LIMIT", "1")
+    monkeypatch.setenv("UOCR_MOE_SPIN_LIMIT", "0")
     failed = n(moe.decode_rows(t(x)))
     monkeypatch.delenv("UOCR_MOE_SPIN_LIMIT")
-    assert np.isnan(failed).any()
+    assert np.isnan(failed).all()
     assert np.isnan(n(moe.decode_rows(t(x)))).all()  # the slot stays poisoned
     assert _lib.fused_errors() == 1  # reported, and cleared
     assert bits_equal(n(moe.decode_rows(t(x))), want)

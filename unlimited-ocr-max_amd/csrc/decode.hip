@@ -62,10 +62,29 @@ constexpr int kThreads = kWaves * kWave;
 constexpr int kXPad = kFusedXPad;
 
 // control words
-constexpr int C_EPOCH = 0, C_ARRIVED = 1, C_COMBINED = 2, C_ERR = 4;
+// Words every workgroup touches are spread over 128-byte lines (kLine words
+// apart): agent-scope loads and atomics skip the L2, and those on one line
+// queue one after another at the memory (256 workgroups on one word cost
+// microseconds, and on this architecture a wave's later waits for its loads
+// also wait for its earlier atomics).
+//   C_EPOCH   + k * kLine, k < kSpread: the epoch, one copy per line;
+//             workgroup b reads copy b % kSpread at its start
+//   C_ARRIVED + k * kLine, k < kSpread: workgroups arrived, workgroup b adds
+//             to counter b % kSpread
+//   C_COMBINED + k * kLine, k < kCombGroups: comb tasks done, comb task c
+//             adds to counter c % kCombGroups; the last of a group adds to
+//             C_COMBINED2, and the last of those is the launch's last comb
+constexpr int kLine = 32, kSpread = 32, kCombGroups = 8;
+constexpr int C_ERR = 4, C_COMBINED2 = kLine, C_EPOCH = 2 * kLine, C_ARRIVED = C_EPOCH + kSpread * kLine,
+              C_COMBINED = C_ARRIVED + kSpread * kLine;
+static_assert(C_COMBINED + kCombGroups * kLine <= kFusedCtlWords, "control words");
 
-// The logits are written to kLogitCopies copies; workgroup b polls copy
-// b % kLogitCopies, so no single memory channel serves every poller.
+// Workgroup b runs on XCD b % kXcds (the dispatcher deals workgroups to the
+// XCDs round robin).  Every XCD computes all the logits itself into its own
+// copy, with workgroup-scope stores that stay in that XCD's L2, where its
+// workgroups' polls find them: the hand-off never waits in the memory's
+// queues behind the weight streams.
+constexpr int kXcds = kFusedXcds;
 constexpr int kLogitCopies = kFusedLogitCopies;
 constexpr int kLogitCopyWords = kFusedLogitCopyWords;
 
@@ -107,19 +126,29 @@ __device__ __forceinline__ uint64_t ld_pair(const uint64_t* p) {
 __device__ __forceinline__ void st_pair(uint64_t* p, float v, uint32_t tag) {
   __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A pair for waves of the same XCD only: the workgroup-scope store stays in the
+// XCD's L2, where their (agent-scope) polls find it without a memory round trip.
+__device__ __forceinline__ void st_pair_xcd(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Sleeps until the constant-rate clock reaches t.
+__device__ __forceinline__ void wait_until(int64_t t) {
+  while ((int64_t)wall_clock64() < t) __builtin_amdgcn_s_sleep(1);
+}
 __device__ __forceinline__ float pair_value(uint64_t q) { return __uint_as_float((uint32_t)q); }
 __device__ __forceinline__ bool pair_has(uint64_t q, uint32_t tag) { return (uint32_t)(q >> 32) == tag; }
 
 // One round of a bounded poll: true once every lane is ready.  `spin` starts
 // at the wait's limit (FusedArgs::spin_limit rounds, tens of milliseconds by
-// default: real waits take microseconds) and counts down.  When it runs out,
+// default: real waits take microseconds; 0 makes every wait fail at once) and
+// counts down.  When it runs out,
 // or once another wait has failed (the error word, read every 8192 rounds), it
 // records an error and lets the wave go on with spin = 0 (expired()): the
 // waiter then takes NaN for the values it waited for, so every output that
 // depends on them is NaN, and the launch still ends.
 __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* ctl) {
-  if (__all(ready)) return true;
-  --spin;  // >= 1 before: a wait that is not ready has not expired yet
+  if (spin != 0u && __all(ready)) return true;  // a limit of 0 fails every wait (the host's test of this path)
+  if (spin != 0u) --spin;
   if (spin == 0u || ((spin & 8191u) == 0u && ld_word(ctl + C_ERR) != 0u)) {
     if (lane() == 0) st_word(ctl + C_ERR, 1u);
     spin = 0u;
@@ -272,7 +301,7 @@ __device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) {
 __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int t, uint32_t tag, int* r_ids,
                                                            float* r_wts, int* r_done) {
   const int l = lane();
-  const uint64_t* src = A.logits + (blockIdx.x % kLogitCopies) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
+  const uint64_t* src = A.logits + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
   uint64_t q;
   uint32_t spin = A.spin_limit;
   const bool wtrace = A.trace != nullptr && t == 0 && l == 0;
@@ -458,14 +487,15 @@ struct Ctx {
   float* act;       // the wave's activation stage
   uint32_t tag;
   int t;            // the running task (tracing)
+  int64_t t_start;  // clock when the wave started
+  int64_t t_routed; // clock when the wave learnt the routing
 };
 
 // Router task of expert e: the lane's router weights (k = l + 64 j), loaded
 // before the x rows are staged, then every token's logit in the 64-lane tree
 // order, stored into each copy of the logits.
 constexpr int kMaxJ = 32;  // H <= 2048
-constexpr int kRouterWaves = 4;   // router tasks per workgroup
-constexpr int kRouterTokens = 2;  // tokens per router task
+constexpr int kRouterWaves = kFusedRouterWaves;  // router tasks per workgroup
 
 __device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A, int e, float (&w)[kMaxJ]) {
   const int l = lane();
@@ -487,7 +517,7 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
     for (int j = 0; j < kMaxJ; ++j)
       if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
     const float v = tree_sum(p);
-    if (l < kLogitCopies) st_pair(A.logits + l * kLogitCopyWords + t * 64 + e, v, C.tag);
+    if (l == 0) st_pair_xcd(A.logits + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + e, v, C.tag);
   }
   if (t0 == 0) UOCR_TRACE(A, C.t, 4);
 }
@@ -504,6 +534,7 @@ __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, c
 
 __device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   Stage<false> st;
+  wait_until(C.t_start + A.sh_delay);
   issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
   UOCR_TRACE_LOADS(A, C.t);
   sgu_rows(A, C, k, st);
@@ -536,6 +567,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   const int l = lane();
   const int g = k.b;
   Stage<false> st;
+  wait_until(C.t_start + A.sh_delay);
   issue_kblocked(A.sh_down, A.H, k.a * 64, g, st);
   UOCR_TRACE_LOADS(A, C.t);
   // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
@@ -645,6 +677,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   const int n0 = k.b * A.c_dn;
   const int ncols = min(A.c_dn, A.H - n0);
   Stage<INT8> st;
+  wait_until(C.t_routed + A.dn_delay);
   issue_routed<INT8>(A, false, e, n0, ncols, st);
   UOCR_TRACE_LOADS(A, C.t);
   const int lanes = ncols * A.gf;
@@ -721,22 +754,35 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   for (int j = 0; j < kMaxK; ++j)
     if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
   A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : acc + shv;
+  // two-level count of the comb tasks: c is this task's ordinal among them
+  const int c = k.a * A.B + t;
+  const int grp = c % kCombGroups;
+  const int in_grp = (A.n_comb - grp + kCombGroups - 1) / kCombGroups;
+  const int groups = min(A.n_comb, kCombGroups);
   uint32_t old = 0;
-  if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED + grp * kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = shfl(old, 0);
-  if (old + 1u == (uint32_t)A.n_comb) {
-    uint32_t spin = A.spin_limit;
-    while (!poll_done(ld_word(A.ctl + C_ARRIVED) >= gridDim.x, spin, A.ctl)) {
-    }
-    // A workgroup that never arrived may still start: the counters and the
-    // epoch then stay as they are (that late workgroup takes this launch's
-    // tag), and the error word keeps later launches' outputs NaN until the
-    // host clears the slot.
-    if (l == 0 && !expired(spin)) {
-      st_word(A.ctl + C_ARRIVED, 0u);
-      st_word(A.ctl + C_COMBINED, 0u);
-      st_word(A.ctl + C_EPOCH, epoch + 1u);
-    }
+  if (old + 1u != (uint32_t)in_grp) return;
+  if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = shfl(old, 0);
+  if (old + 1u != (uint32_t)groups) return;
+  // the launch's last comb task: once every workgroup has read the epoch, reset
+  // the counters and advance it
+  uint32_t spin = A.spin_limit;
+  for (;;) {
+    const uint32_t arrived = l < kSpread ? ld_word(A.ctl + C_ARRIVED + l * kLine) : 0u;
+    if (poll_done(tree_sum_u32(arrived) >= gridDim.x, spin, A.ctl)) break;
+  }
+  // A workgroup that never arrived may still start: the counters and the
+  // epoch then stay as they are (that late workgroup takes this launch's tag),
+  // and the error word keeps later launches' outputs NaN until the host clears
+  // the slot.
+  if (expired(spin)) return;
+  if (l < kSpread) {
+    st_word(A.ctl + C_ARRIVED + l * kLine, 0u);
+    if (l < kCombGroups) st_word(A.ctl + C_COMBINED + l * kLine, 0u);
+    if (l == 0) st_word(A.ctl + C_COMBINED2, 0u);
+    st_word(A.ctl + C_EPOCH + l * kLine, epoch + 1u);
   }
 }
 
@@ -786,43 +832,74 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   C.r_ids = r_ids;
   C.r_wts = r_wts;
   C.act = (float*)(lds + A.lds_x + 528 + wave * A.lds_act);
-  const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_word(A.ctl + C_EPOCH));
-  C.tag = epoch + 1u;
   const int nwaves = (int)gridDim.x * kWaves;
   const int rank = wave * (int)gridDim.x + (int)blockIdx.x;
-  // Router task i (expert i % E, tokens 2(i / E) and 2(i / E) + 1) runs on
-  // wave i % 4 of workgroup i / 4: workgroups that start early (the grid's
-  // start is spread over about a microsecond, and every routing waits for
-  // the last logit), few enough router rows per CU that their loads do not
-  // queue behind each other.  Every wave then takes the rest of the task
-  // list from E + rank on.
-  const int re = (int)blockIdx.x * kRouterWaves + wave;
-  const int n_router = A.E * ((A.B + kRouterTokens - 1) / kRouterTokens);
+  C.t_start = (int64_t)wall_clock64();
+  C.t_routed = C.t_start;
+  if (A.trace != nullptr && threadIdx.x == 0) A.trace[A.trace_wg + blockIdx.x * 8 + 6] = C.t_start;
+  // Every XCD computes all the logits: its router task i (expert i % E,
+  // tokens r_tok * (i / E) onwards) runs on wave i % kRouterWaves of its
+  // (i / kRouterWaves)-th workgroup, the XCD's first workgroups (the grid's
+  // start is spread over about a microsecond, and every routing waits for the
+  // last logit).  Every wave then takes the rest of the task list from
+  // E + rank on.
+  const int re = ((int)blockIdx.x / kXcds) * kRouterWaves + wave;
+  const int n_router = A.E * ((A.B + A.r_tok - 1) / A.r_tok);
   const bool router = wave < kRouterWaves && re < n_router;
   const int r_e = re % A.E;
-  const int r_t0 = (re / A.E) * kRouterTokens;
+  const int r_t0 = (re / A.E) * A.r_tok;
   int t = A.E + rank;
 
   // a router task's weights do not depend on x: they load while x is staged
   float w[kMaxJ];
   if (router) router_load(A, r_e, w);
 
-  // x rows into LDS, each 128-element chunk padded to kXPad floats
-  for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
-    const int r = i / A.H;
-    const int kk = i - r * A.H;
-    xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
+  // x rows into LDS, each 128-element chunk padded to kXPad floats: every
+  // thread's loads are issued before the first is used (one memory latency,
+  // not one per pass over the rows)
+  {
+    constexpr int kXPasses = (8 * 2048 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
+    const int n = A.B * A.H;
+    float xv[kXPasses];
+#pragma unroll
+    for (int j = 0; j < kXPasses; ++j) {
+      const int i = (int)threadIdx.x + j * kThreads;
+      xv[j] = i < n ? ldg(A.x + i) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kXPasses; ++j) {
+      const int i = (int)threadIdx.x + j * kThreads;
+      if (i < n) {
+        const int r = i / A.H;
+        const int kk = i - r * A.H;
+        xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = xv[j];
+      }
+    }
   }
-  if (threadIdx.x == 0) *r_done = 0;
+  // One load of the epoch per workgroup (3 072 waves loading the one word at
+  // once would queue every workgroup's start behind it), shared through LDS.
+  uint32_t* lds_epoch = (uint32_t*)(lds + A.lds_x + 516);
+  if (threadIdx.x == 0) {
+    *r_done = 0;
+    *lds_epoch = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
+    if (A.trace != nullptr) {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      A.trace[A.trace_wg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
+    }
+  }
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(A.ctl + C_ARRIVED, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t epoch = __builtin_amdgcn_readfirstlane(*lds_epoch);
+  C.tag = epoch + 1u;
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(A.ctl + C_ARRIVED + (blockIdx.x % kSpread) * kLine, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 
   if (router) {
-    // the trace keeps one record per expert: its first tokens' task
-    const bool traced = r_t0 == 0;
+    // the trace keeps one record per expert: XCD 0's task of its first tokens
+    const bool traced = r_t0 == 0 && blockIdx.x % kXcds == 0;
     C.t = r_e;
     if (traced) UOCR_TRACE(A, r_e, 0);
-    router_task(A, C, r_e, r_t0, min(A.B, r_t0 + kRouterTokens), w);
+    router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
     if (traced) UOCR_TRACE(A, r_e, 2);
     if (traced && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
   }
@@ -844,7 +921,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
                         A.ctl)) {
       }
       asm volatile("" ::: "memory");
-      if (A.trace != nullptr) troute = (int64_t)wall_clock64();
+      C.t_routed = (int64_t)wall_clock64();
+      if (A.trace != nullptr) troute = C.t_routed;
       // without the routing (a failed wait), no routed task runs: the combine's waits for them fail too
       rt = expired(spin) ? Route{0ull, 0, r_ids, 0} : make_route(A, r_ids);
       n_tasks = task_count(A, rt.ng);
@@ -907,8 +985,9 @@ hipError_t fused_grid(size_t lds_bytes, int* grid) {
 }
 
 hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
-  // every router task needs its workgroup (the routing waits for all logits)
-  if ((int64_t)grid * kRouterWaves < (int64_t)a.E * ((a.B + kRouterTokens - 1) / kRouterTokens))
+  // every XCD runs all router tasks on its own workgroups (the routing waits for all logits)
+  if (grid % kXcds != 0 || a.r_tok < 1 ||
+      (int64_t)(grid / kXcds) * kRouterWaves < (int64_t)a.E * ((a.B + a.r_tok - 1) / a.r_tok))
     return hipErrorInvalidConfiguration;
   UOCR_LAUNCH("decode_fused", k_decode_fused, dim3(grid), dim3(kThreads), lds_bytes, s, a);
   return hipGetLastError();

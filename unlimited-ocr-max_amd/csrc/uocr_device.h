@@ -242,6 +242,15 @@ __device__ __forceinline__ uint32_t tree_umax(uint32_t v) {
   v = max(v, from_up<1>(v));
   return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
+__device__ __forceinline__ uint32_t tree_sum_u32(uint32_t v) {
+  v += from_up<32>(v);
+  v += from_up<16>(v);
+  v += from_up<8>(v);
+  v += from_up<4>(v);
+  v += from_up<2>(v);
+  v += from_up<1>(v);
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
 __device__ __forceinline__ uint32_t tree_or(uint32_t v) {
   v |= from_up<32>(v);
   v |= from_up<16>(v);

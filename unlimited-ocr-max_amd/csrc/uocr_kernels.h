@@ -225,7 +225,10 @@ hipError_t launch_paged_attention(const PagedAttention& p, hipStream_t s);
 
 constexpr int kFusedWaves = 12;  // waves per workgroup, one workgroup per CU (168 VGPRs a lane)
 constexpr int kFusedXPad = 132;  // floats per 128-element chunk of an LDS activation row
-constexpr int kFusedLogitCopies = 16;      // copies of the tagged logits
+constexpr int kFusedCtlWords = 2368;      // control words per slot: error word, epoch copies, counters
+constexpr int kFusedXcds = 8;              // XCDs of the device (workgroup b runs on XCD b % 8)
+constexpr int kFusedLogitCopies = kFusedXcds;  // copies of the tagged logits, one per XCD
+constexpr int kFusedRouterWaves = 4;       // router tasks per workgroup
 constexpr int kFusedLogitCopyWords = 576;  // 64-bit words per copy (8 tokens x 64 experts, padded)
 
 // Task layout, LDS and tagged-buffer sizes of one layer shape.
@@ -274,6 +277,10 @@ struct FusedArgs {
   float inv_gh, inv_gf;
   // polls a wait may take before it fails (sets the error word, takes NaN)
   uint32_t spin_limit;
+  int r_tok;  // tokens per router task
+  // clock ticks (100 MHz) that shared tasks wait after the wave's start, and
+  // routed down tasks after the routing, before loading their weights
+  uint32_t sh_delay, dn_delay;
   // optional per-task phase timestamps (8 words per task), null when off;
   // per-workgroup words start at trace_wg
   int64_t* trace;

@@ -130,7 +130,6 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
 // capture; a stream first seen under capture takes a spare slot, or the call is
 // refused.  No slot is shared by two streams, and nothing is freed before
 // uocr_moe_release(), so graphs captured earlier keep valid pointers.
-constexpr int kFusedCtlWords = 64;
 constexpr int kFusedChunk = 4;
 constexpr int C_ERR_WORD = 4;  // the kernel's error word (decode.hip)
 struct FusedSlot {
@@ -764,15 +763,27 @@ static bool fused_eligible(const uocr_moe_layer* L, int64_t B) {
 }
 
 // Polls per bounded wait of the persistent kernel: 2^16 (tens of milliseconds;
-// healthy waits take microseconds).  UOCR_MOE_SPIN_LIMIT (>= 1) overrides it, so
-// a test can make the waits run out and check the failure path.
+// healthy waits take microseconds).  UOCR_MOE_SPIN_LIMIT overrides it, so a
+// test can make the waits run out and check the failure path (0: every wait
+// fails at once, even one whose data is there).
 static uint32_t fused_spin_limit() {
   const char* env = std::getenv("UOCR_MOE_SPIN_LIMIT");
   if (env != nullptr) {
     const long v = std::strtol(env, nullptr, 10);
-    if (v >= 1 && v <= (1L << 30)) return (uint32_t)v;
+    if (v >= 0 && v <= (1L << 30)) return (uint32_t)v;
   }
   return 1u << 16;
+}
+
+// A delay of the persistent kernel in 100 MHz clock ticks: `def`, or the
+// environment variable `name` (0..100000) for measurements.
+static uint32_t fused_env_ticks(const char* name, uint32_t def) {
+  const char* env = std::getenv(name);
+  if (env != nullptr) {
+    const long v = std::strtol(env, nullptr, 10);
+    if (v >= 0 && v <= 100000) return (uint32_t)v;
+  }
+  return def;
 }
 
 static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayout& lay, const FusedSlot& f) {
@@ -820,6 +831,8 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.inv_gh = 1.0f / (float)lay.gh;
   a.inv_gf = 1.0f / (float)lay.gf;
   a.spin_limit = fused_spin_limit();
+  a.sh_delay = fused_env_ticks("UOCR_MOE_SH_DELAY", 0);
+  a.dn_delay = fused_env_ticks("UOCR_MOE_DN_DELAY", 0);
   return a;
 }
 
@@ -922,6 +935,15 @@ static int decode_rows_impl(const char* op, float* out, const float* x, int64_t 
     if (e != hipSuccess) return hip_fail(err, errlen, op, e);
     if (grid < 1) return fail(err, errlen, "%s: the persistent decode kernel does not fit a CU", op);
     FusedArgs a = fused_args(L, B, lay, slot);
+    // tokens per router task: every XCD computes all E x B logits on kFusedRouterWaves waves of each of its
+    // workgroups
+    const int64_t router_slots = (int64_t)(grid / kFusedXcds) * kFusedRouterWaves;
+    const int64_t xcd_experts = L->num_experts;
+    a.r_tok = 1;
+    while (a.r_tok < B && xcd_experts * ((B + a.r_tok - 1) / a.r_tok) > router_slots) ++a.r_tok;
+    if (grid % kFusedXcds != 0 || xcd_experts * ((B + a.r_tok - 1) / a.r_tok) > router_slots)
+      return fail(err, errlen, "%s: the persistent decode kernel needs a grid of whole XCDs with room for its "
+                  "router tasks", op);
     a.x = x;
     a.out = out;
     a.ids_out = expert_ids;
