@@ -313,7 +313,9 @@ int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errl
  * arrived, 3 activations ready, 4 chain done, 5 counter updated, 6 end) and
  * word 7 the wave that ran it.  grid_waves receives the waves of the last
  * launch configuration.  A diagnostic of this build's decode kernel; tracing
- * waits for each task's loads, so a traced launch runs slower. */
+ * waits for each task's loads, so a traced launch runs slower.  The trace is
+ * compiled in only when the library is built with UOCR_DECODE_TRACE=1; other
+ * builds refuse the call. */
 int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err, size_t errlen);
 
 /* ---------------------------------------------------------------------------

@@ -12,19 +12,20 @@
 // tasks dealt round robin to the waves (task t to the wave of rank t mod
 // waves, ranks interleaved across workgroups so neighbouring tasks land on
 // different CUs and XCDs), every wave walking its tasks in increasing order:
-//   router  one expert's logits for every token                       (E)
+//   router  one expert's logits for a few tokens (on every XCD)      (E x tokens / r_tok)
 //   sgu     shared gate or up: 64 columns x one 128-chunk of H         (Fs/64 x 2 x H/128)
-//   sfold   shared gate/up partials of 64 columns, one token -> SwiGLU
-//           -> hs                                                      (Fs/64 x B)
-//   sdn     shared down: 64 columns x one 128-chunk of Fs              (H/64 x Fs/128)
 //   rgu     routed gate+up of one selected expert: a few columns,
 //           every chunk of H (lane = column, projection, chunk)        (experts x F/c_gu)
 //   rdn     routed down of one selected expert: a few columns, every
 //           chunk of F (lane = column, chunk)                          (experts x H/c_dn)
+//   sfold   shared gate/up partials of 64 columns, one token -> SwiGLU
+//           -> hs                                                      (Fs/64 x B)
+//   sdn     shared down: 64 columns x one 128-chunk of Fs              (H/64 x Fs/128)
 //   comb    64 columns, one token: shared-down partials -> sh, then the
 //           weighted combine of the token's routed rows plus sh        (H/64 x B)
-// The tasks before rgu need no routing: a wave runs those of its tasks while
-// the routing is computed.  A routed task holds every chunk of its columns, so
+// The sgu tasks need no routing: a wave runs those while the routing is
+// computed.  The tasks that wait for other tasks' results (sfold, sdn, comb)
+// come last, so that no routed task is queued behind such a wait.  A routed task holds every chunk of its columns, so
 // its per-group fold runs
 // inside the wave (lane shuffles); only the shared experts, whose chunks are
 // spread over tasks, fold partials written by other waves.  Each lane loads
@@ -131,10 +132,6 @@ __device__ __forceinline__ void st_pair(uint64_t* p, float v, uint32_t tag) {
 __device__ __forceinline__ void st_pair_xcd(uint64_t* p, float v, uint32_t tag) {
   __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-// Sleeps until the constant-rate clock reaches t.
-__device__ __forceinline__ void wait_until(int64_t t) {
-  while ((int64_t)wall_clock64() < t) __builtin_amdgcn_s_sleep(1);
-}
 __device__ __forceinline__ float pair_value(uint64_t q) { return __uint_as_float((uint32_t)q); }
 __device__ __forceinline__ bool pair_has(uint64_t q, uint32_t tag) { return (uint32_t)(q >> 32) == tag; }
 
@@ -196,16 +193,24 @@ __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, in
 // at least 1/(2d) away from the next integer, far beyond the rounding error.
 __device__ __forceinline__ int small_div(int x, float inv) { return (int)(((float)x + 0.5f) * inv); }
 
+// The phase trace (uocr_moe_fused_trace) is compiled in only with
+// UOCR_DECODE_TRACE=1: every launch starts with cold instruction caches, so
+// code on the paths each workgroup runs once costs a fetch per cache line.
+#ifndef UOCR_DECODE_TRACE
+#define UOCR_DECODE_TRACE 0
+#endif
+constexpr bool kTrace = UOCR_DECODE_TRACE != 0;
+
 // Phase timestamps of a task (the constant-rate wall clock), when tracing:
 // 0 start, 1 weights landed (waited for only when tracing), 3 inputs polled,
 // 4 chains done, 2 end, 5 when the wave learnt the routing, 7 the wave.
 #define UOCR_TRACE(a, task, slot)                                                                          \
   do {                                                                                                     \
-    if ((a).trace != nullptr && lane() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
+    if (kTrace && (a).trace != nullptr && lane() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
   } while (0)
 #define UOCR_TRACE_LOADS(a, task)                       \
   do {                                                  \
-    if ((a).trace != nullptr) {                         \
+    if (kTrace && (a).trace != nullptr) {                         \
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); \
       UOCR_TRACE(a, task, 1);                           \
     }                                                   \
@@ -226,9 +231,15 @@ __device__ __forceinline__ int task_count(const KA FusedArgs& A, int ng) {
   return A.E + A.n_sgu + A.n_sfold + A.n_sdn + ng * A.per_e_gu + ng * A.per_e_dn + A.n_comb;
 }
 
-// Tasks that do not need the routing: the router, and the shared experts.
-__device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.E + A.n_sgu + A.n_sfold + A.n_sdn; }
+// Tasks before the routed ones: the router, and the shared gate/up partials
+// (which wait for nothing).  The shared folds and down partials, which wait
+// for other tasks, come after the routed tasks, so that a wave's routed work
+// is never queued behind such a wait: a wave's second task is then one whose
+// inputs come late anyway.
+__device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.E + A.n_sgu; }
 
+// Task order: router, sgu, rgu, rdn, sfold, sdn, comb (every task waits only
+// for tasks before it).
 __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
   if (t < A.E) return {K_ROUTER, t, 0, 0};
   t -= A.E;
@@ -240,16 +251,6 @@ __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
     return {K_SGU, u, p, r - p * A.gh};
   }
   t -= A.n_sgu;
-  if (t < A.n_sfold) {
-    const int u = t / A.B;
-    return {K_SFOLD, u, t - u * A.B, 0};
-  }
-  t -= A.n_sfold;
-  if (t < A.n_sdn) {
-    const int cb = t / A.gfs;
-    return {K_SDN, cb, t - cb * A.gfs, 0};
-  }
-  t -= A.n_sdn;
   if (t < ng * A.per_e_gu) {
     const int s = t / A.per_e_gu;
     return {K_RGU, s, t - s * A.per_e_gu, 0};
@@ -260,6 +261,16 @@ __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
     return {K_RDN, s, t - s * A.per_e_dn, 0};
   }
   t -= ng * A.per_e_dn;
+  if (t < A.n_sfold) {
+    const int u = t / A.B;
+    return {K_SFOLD, u, t - u * A.B, 0};
+  }
+  t -= A.n_sfold;
+  if (t < A.n_sdn) {
+    const int cb = t / A.gfs;
+    return {K_SDN, cb, t - cb * A.gfs, 0};
+  }
+  t -= A.n_sdn;
   if (t < A.n_comb) {
     const int cb = t / A.B;
     return {K_COMB, cb, t - cb * A.B, 0};
@@ -304,7 +315,7 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   const uint64_t* src = A.logits + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
   uint64_t q;
   uint32_t spin = A.spin_limit;
-  const bool wtrace = A.trace != nullptr && t == 0 && l == 0;
+  const bool wtrace = kTrace && A.trace != nullptr && t == 0 && l == 0;
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 0] = (int64_t)wall_clock64();
   do {
     q = ld_pair(src);
@@ -487,8 +498,6 @@ struct Ctx {
   float* act;       // the wave's activation stage
   uint32_t tag;
   int t;            // the running task (tracing)
-  int64_t t_start;  // clock when the wave started
-  int64_t t_routed; // clock when the wave learnt the routing
 };
 
 // Router task of expert e: the lane's router weights (k = l + 64 j), loaded
@@ -534,7 +543,6 @@ __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, c
 
 __device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   Stage<false> st;
-  wait_until(C.t_start + A.sh_delay);
   issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
   UOCR_TRACE_LOADS(A, C.t);
   sgu_rows(A, C, k, st);
@@ -567,7 +575,6 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   const int l = lane();
   const int g = k.b;
   Stage<false> st;
-  wait_until(C.t_start + A.sh_delay);
   issue_kblocked(A.sh_down, A.H, k.a * 64, g, st);
   UOCR_TRACE_LOADS(A, C.t);
   // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
@@ -677,7 +684,6 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   const int n0 = k.b * A.c_dn;
   const int ncols = min(A.c_dn, A.H - n0);
   Stage<INT8> st;
-  wait_until(C.t_routed + A.dn_delay);
   issue_routed<INT8>(A, false, e, n0, ncols, st);
   UOCR_TRACE_LOADS(A, C.t);
   const int lanes = ncols * A.gf;
@@ -792,7 +798,7 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
   Ctx C = C0;
   C.t = t;
   UOCR_TRACE(A, t, 0);
-  if (A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 5] = troute;
+  if (kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 5] = troute;
   switch (k.kind) {
     case K_SGU: task_sgu(A, C, k); break;
     case K_RGU:
@@ -813,7 +819,7 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
     default: break;
   }
   UOCR_TRACE(A, t, 2);
-  if (A.trace != nullptr && lane() == 0)
+  if (kTrace && A.trace != nullptr && lane() == 0)
     A.trace[(int64_t)t * 8 + 7] = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
 }
 
@@ -834,9 +840,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   C.act = (float*)(lds + A.lds_x + 528 + wave * A.lds_act);
   const int nwaves = (int)gridDim.x * kWaves;
   const int rank = wave * (int)gridDim.x + (int)blockIdx.x;
-  C.t_start = (int64_t)wall_clock64();
-  C.t_routed = C.t_start;
-  if (A.trace != nullptr && threadIdx.x == 0) A.trace[A.trace_wg + blockIdx.x * 8 + 6] = C.t_start;
+  if (kTrace && A.trace != nullptr && threadIdx.x == kThreads - kWave)
+    A.trace[A.trace_wg + blockIdx.x * 8 + 6] = (int64_t)wall_clock64();
   // Every XCD computes all the logits: its router task i (expert i % E,
   // tokens r_tok * (i / E) onwards) runs on wave i % kRouterWaves of its
   // (i / kRouterWaves)-th workgroup, the XCD's first workgroups (the grid's
@@ -854,35 +859,44 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   float w[kMaxJ];
   if (router) router_load(A, r_e, w);
 
-  // x rows into LDS, each 128-element chunk padded to kXPad floats: every
-  // thread's loads are issued before the first is used (one memory latency,
-  // not one per pass over the rows)
-  {
-    constexpr int kXPasses = (8 * 2048 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
-    const int n = A.B * A.H;
-    float xv[kXPasses];
+  // x rows into LDS, each 128-element chunk padded to kXPad floats: 16-byte
+  // pieces (a chunk is 32 of them), every thread's loads issued before the
+  // first is used, in little code (each launch runs it with cold caches)
+  if (A.x_vec) {
+    constexpr int kXPasses = (8 * 2048 / 4 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
+    const int n4 = A.B * A.H / 4;
+    f32x4 xv[kXPasses];
 #pragma unroll
     for (int j = 0; j < kXPasses; ++j) {
       const int i = (int)threadIdx.x + j * kThreads;
-      xv[j] = i < n ? ldg(A.x + i) : 0.0f;
+      if (i < n4) xv[j] = *(const UOCR_GLOBAL f32x4*)(A.x + 4 * i);
     }
 #pragma unroll
     for (int j = 0; j < kXPasses; ++j) {
       const int i = (int)threadIdx.x + j * kThreads;
-      if (i < n) {
-        const int r = i / A.H;
-        const int kk = i - r * A.H;
-        xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = xv[j];
+      if (i < n4) {
+        const int r = (4 * i) / A.H;
+        const int kk = 4 * i - r * A.H;
+        *(f32x4*)(xs + r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)) = xv[j];
       }
+    }
+  } else {
+    for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
+      const int r = i / A.H;
+      const int kk = i - r * A.H;
+      xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
     }
   }
   // One load of the epoch per workgroup (3 072 waves loading the one word at
   // once would queue every workgroup's start behind it), shared through LDS.
+  // The last wave does it (and the arrival count below): its first work is
+  // to wait for the logits, while the router tasks run on the first waves.
+  constexpr int kCtlThread = kThreads - kWave;
   uint32_t* lds_epoch = (uint32_t*)(lds + A.lds_x + 516);
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == kCtlThread) {
     *r_done = 0;
     *lds_epoch = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
-    if (A.trace != nullptr) {
+    if (kTrace && A.trace != nullptr) {
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       A.trace[A.trace_wg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
     }
@@ -890,7 +904,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   __syncthreads();
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(*lds_epoch);
   C.tag = epoch + 1u;
-  if (threadIdx.x == 0)
+  if (threadIdx.x == kCtlThread)
     __hip_atomic_fetch_add(A.ctl + C_ARRIVED + (blockIdx.x % kSpread) * kLine, 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 
@@ -901,7 +915,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     if (traced) UOCR_TRACE(A, r_e, 0);
     router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
     if (traced) UOCR_TRACE(A, r_e, 2);
-    if (traced && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
+    if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
   }
   // The routing of token i is computed by wave kWaves-1-i (high waves, whose
   // tasks come late in the list); the other waves meanwhile run their tasks
@@ -921,8 +935,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
                         A.ctl)) {
       }
       asm volatile("" ::: "memory");
-      C.t_routed = (int64_t)wall_clock64();
-      if (A.trace != nullptr) troute = C.t_routed;
+      if (kTrace && A.trace != nullptr) troute = (int64_t)wall_clock64();
       // without the routing (a failed wait), no routed task runs: the combine's waits for them fail too
       rt = expired(spin) ? Route{0ull, 0, r_ids, 0} : make_route(A, r_ids);
       n_tasks = task_count(A, rt.ng);
@@ -971,6 +984,8 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
   L.data_words = L.off_psdn + (int64_t)L.cb_h * L.gfs * 8 * 64;
   return L;
 }
+
+bool fused_trace_built() { return kTrace; }
 
 hipError_t fused_grid(size_t lds_bytes, int* grid) {
   int dev = 0, cus = 0, per_cu = 0;

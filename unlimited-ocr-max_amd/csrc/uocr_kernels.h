@@ -278,15 +278,14 @@ struct FusedArgs {
   // polls a wait may take before it fails (sets the error word, takes NaN)
   uint32_t spin_limit;
   int r_tok;  // tokens per router task
-  // clock ticks (100 MHz) that shared tasks wait after the wave's start, and
-  // routed down tasks after the routing, before loading their weights
-  uint32_t sh_delay, dn_delay;
+  int x_vec;  // x is 16-byte aligned
   // optional per-task phase timestamps (8 words per task), null when off;
   // per-workgroup words start at trace_wg
   int64_t* trace;
   int64_t trace_wg;
 };
 hipError_t fused_grid(size_t lds_bytes, int* grid);
+bool fused_trace_built();  // the kernel was compiled with its phase trace (UOCR_DECODE_TRACE=1)
 hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t s);
 

@@ -775,17 +775,6 @@ static uint32_t fused_spin_limit() {
   return 1u << 16;
 }
 
-// A delay of the persistent kernel in 100 MHz clock ticks: `def`, or the
-// environment variable `name` (0..100000) for measurements.
-static uint32_t fused_env_ticks(const char* name, uint32_t def) {
-  const char* env = std::getenv(name);
-  if (env != nullptr) {
-    const long v = std::strtol(env, nullptr, 10);
-    if (v >= 0 && v <= 100000) return (uint32_t)v;
-  }
-  return def;
-}
-
 static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayout& lay, const FusedSlot& f) {
   FusedArgs a{};
   a.B = (int)B;
@@ -831,8 +820,6 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.inv_gh = 1.0f / (float)lay.gh;
   a.inv_gf = 1.0f / (float)lay.gf;
   a.spin_limit = fused_spin_limit();
-  a.sh_delay = fused_env_ticks("UOCR_MOE_SH_DELAY", 0);
-  a.dn_delay = fused_env_ticks("UOCR_MOE_DN_DELAY", 0);
   return a;
 }
 
@@ -945,6 +932,7 @@ static int decode_rows_impl(const char* op, float* out, const float* x, int64_t 
       return fail(err, errlen, "%s: the persistent decode kernel needs a grid of whole XCDs with room for its "
                   "router tasks", op);
     a.x = x;
+    a.x_vec = aligned16(x) ? 1 : 0;
     a.out = out;
     a.ids_out = expert_ids;
     a.wts_out = expert_weights;
@@ -1274,8 +1262,9 @@ int uocr_moe_timing_end(int capacity, float* ms, char* names, size_t name_stride
 }
 
 int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err, size_t errlen) {
-  (void)err;
-  (void)errlen;
+  if (!fused_trace_built())
+    return fail(err, errlen, "uocr_moe_fused_trace: the library was built without the decode phase trace "
+                "(build with UOCR_DECODE_TRACE=1)");
   std::lock_guard<std::mutex> lock(g_ws_mu);
   if (grid_waves) *grid_waves = g_trace_grid * kFusedWaves;
   g_trace = static_cast<int64_t*>(buffer);
