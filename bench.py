@@ -640,7 +640,7 @@ def _by_name(part: str) -> Callable[[list], list]:
 def prefill_gemm_dispatches(rows: list) -> dict[str, list]:
     """The prefill probe's GEMM dispatches by workload, in its launch order: T=512 over the 11 layers, then
     T=4096 and the adversarial T=4096 over 4 layers each; gate/up and down alternate within a layer."""
-    gemms = [r for r in rows if "k_gemm_pair" in r[1]]
+    gemms = [r for r in rows if "k_moe_gemm" in r[1]]
     n512, n4k = 2 * LAYERS, 2 * PREFILL_4K_LAYERS
     groups = {"t512": gemms[:n512], "t4096": gemms[n512:n512 + n4k], "t4096_adversarial": gemms[n512 + n4k:]}
     out = {}

@@ -9,6 +9,17 @@
 // writes h in bf16, already packed in group order, which is the down launch's
 // A operand.  The shared experts (K-blocked bf16) ride in the same launches as
 // extra tiles with every token as a row.
+//
+// Two kernels share the tiling: the LDS-staged one (16-byte aligned weights,
+// the product path) and the fragment-load one (weights at any alignment);
+// both run the same MFMA sequence on the same values, so they give the same
+// bits.  On gfx950 the int8 dequantisation (a conversion, a multiply and half
+// a pack per weight, once per row tile) issues in turn with the MFMAs on a
+// SIMD -- a second wave does not overlap them -- so the int8 kernels are
+// bounded by that issue time; the tiles are sized to spread each dequantised
+// weight over as many rows as the expert has (up to 128).
+#include <atomic>
+
 #include "uocr_device.h"
 #include "uocr_kernels.h"
 
@@ -97,156 +108,122 @@ __global__ void __launch_bounds__(256) k_quantize(int8_t* __restrict__ q, float*
 
 // ------------------------------------------------------------- grouped GEMM
 //
-// A workgroup owns a BM-row tile of one expert's rows (or of the tokens, for
-// the shared experts) and 128 weight rows: 64 columns of both gate and up
-// (SwiGLU launch) or 128 columns of down.  Its waves form a (BM/32) x 2 grid,
-// each computing 32 rows x 32 columns of both projections (or 32 x 64 of
-// down) with v_mfma_f32_32x32x16_bf16.  K advances in steps of BK = 128 (one
-// int8 quantisation group of 128, or half of one of 256, ...): the raw global
-// data of step k+1 (bf16 activations, int8 or bf16 weights and the step's
-// scales) is loaded into registers while the matrix cores work on step k,
-// then converted (weights to bf16_rne(f32(q) * scale)) into the single LDS
-// tile.  Workgroups are dealt to XCDs so that all column tiles of one row
-// tile run on the same XCD: the activation tile they share stays in its L2.
+// C[rows, cols] = A[rows, K] . W[cols, K]^T with v_mfma_f32_32x32x16_bf16
+// (fp32 accumulation): A is bf16 (the gathered x rows for gate/up, h in group
+// order for down, the tokens for the shared experts), W one expert's weight
+// rows (int8 + per-group scales, bf16, or the shared experts' K-blocked bf16).
+//
+// Tile.  A workgroup of 4 waves owns BM rows x 256 weight rows.  Wave w owns
+// weight rows [64w, 64w + 64) as two 32-row MFMA blocks, against all BM rows:
+// every weight is loaded and dequantised by exactly one wave, once per row
+// tile, and each dequantised fragment feeds BM/32 x 2 MFMAs.  The
+// fragment-load kernel (below) reads the weights straight into B-operand
+// registers; the LDS-staged kernel (further below) streams them through LDS.  In the gate/up launch block 0
+// holds gate columns n0 + 32w .. +32 and block 1 the same up columns, so
+// SwiGLU pairs the registers of one lane.  K advances in steps of 64: the A
+// step (BM x 64 bf16) goes global -> registers -> LDS (two buffers, one
+// barrier per step; 16-byte chunks XOR-swizzled by row so that the fragment
+// reads are free of bank conflicts); the weight and A steps are both loaded
+// kWStages steps ahead.  Inside a step, lane half h covers
+// k = 32h .. 32h + 31 in both operands: the MFMA's k order is a permutation of
+// the step's 64, the same for A and W.
+//
+// Placement.  A problem's tiles are (group, column tile, row tile).  Each
+// group's column tiles are cut into ranges (two per routed expert, up to
+// eight for the shared experts); range r of the problem goes to XCD r % 8,
+// whose workgroups walk their XCD's tiles range by range, row tile major and
+// column tile minor.  A range's weight tiles are fetched into one L2 and serve
+// all of its row tiles there, and an A row tile serves the range's column
+// tiles back to back.  The grid is persistent (a fixed number of workgroups
+// per XCD strides through that XCD's list), so no bound on the routing is
+// needed at launch.
 
-constexpr int BK = 128;
-constexpr int kRow = BK + 8;   // bf16 per LDS row (272 bytes: rows 4 banks apart)
-constexpr int kBRows = 128;    // weight rows per workgroup
-constexpr int kWN = kBRows / 64;  // waves along the columns
+constexpr int BK = 64;                    // K per step
+constexpr int kGThreads = 256;            // 4 waves
 constexpr int kXcds = 8;
+constexpr int kWRowsWave = 64;            // weight rows per wave
+constexpr int kWRowsWg = 4 * kWRowsWave;  // weight rows per workgroup
 
-template <int BM>
-struct Geo {
-  static constexpr int kWaves = BM / 32 * kWN;
-  static constexpr int kThreads = kWaves * 64;
-};
+template <WKind W>
+constexpr int kWStages = W == kInt8Rows ? 4 : 2;  // weight steps in flight
 
 struct TileRef {
-  int valid;
   int e;     // expert (routed) or 0
-  int pos0;  // first row position of the tile (group order) or first token
-  int rows;  // valid rows in the tile
+  int pos0;  // first row position (group order) or first token
+  int rows;  // valid rows
   int n0;    // first output column
 };
 
-// The tile of workgroup `wg` of a problem with `mtiles` row tiles and `ntiles`
-// column tiles of width bn: workgroup w runs on XCD w % 8, and XCD x takes
-// the row tiles x, x+8, ... with all their column tiles in turn.
+// The cut of a problem's column tiles into ranges.
+struct Plan {
+  int nt;   // column tiles
+  int per;  // column tiles per range
+  int nr;   // ranges per group
+  int ng;   // groups
+};
+
+__device__ __forceinline__ Plan plan_of(const GemmProblem& P, int bn) {
+  Plan p;
+  const bool routed = P.rows.n_groups != nullptr;
+  p.nt = (P.N + bn - 1) / bn;
+  p.per = routed ? (p.nt + 1) / 2 : (p.nt + kXcds - 1) / kXcds;
+  p.nr = (p.nt + p.per - 1) / p.per;
+  p.ng = routed ? ldc(P.rows.n_groups) : (P.M > 0 ? 1 : 0);
+  return p;
+}
+
 template <int BM>
-__device__ TileRef locate(const GemmProblem& P, int wg, int bn) {
-  TileRef t{0, 0, 0, 0, 0};
-  const int ntiles = P.N / bn;
-  const int x = wg % kXcds;
-  const int j = wg / kXcds;  // the j-th workgroup of XCD x
-  const int mt = x + kXcds * (j / ntiles);
-  t.n0 = (j % ntiles) * bn;
+__device__ __forceinline__ int row_tiles(const GemmProblem& P, int g) {
+  if (P.rows.n_groups == nullptr) return (P.M + BM - 1) / BM;
+  return (ldg(P.rows.group_start + g + 1) - ldg(P.rows.group_start + g) + BM - 1) / BM;
+}
+
+// Lane q: the inclusive prefix of the tile counts of XCD x's ranges x, x + 8,
+// ... (range r: group r / nr, column tiles from (r % nr) * per); the host
+// keeps ng * nr <= 8 * 64.
+template <int BM>
+__device__ int xcd_prefix(const GemmProblem& P, const Plan& p, int x) {
+  const int q = lane_id();
+  const int r = x + kXcds * q;
+  int n = 0;
+  if (r < p.ng * p.nr) {
+    const int g = r / p.nr;
+    const int c = r - g * p.nr;
+    n = row_tiles<BM>(P, g) * min(p.per, p.nt - c * p.per);
+  }
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_up(n, off, kWave);
+    if (q >= off) n += v;
+  }
+  return n;
+}
+
+// Tile `it` of XCD x's list (prefix from xcd_prefix).
+template <int BM>
+__device__ TileRef tile_at(const GemmProblem& P, const Plan& p, int x, int prefix, int it, int bn) {
+  const int q = (int)__popcll(__ballot(prefix <= it));
+  const int before = q > 0 ? __builtin_amdgcn_readlane(prefix, q - 1) : 0;
+  const int r = x + kXcds * q;
+  const int g = r / p.nr;
+  const int c = r - g * p.nr;
+  const int cols = min(p.per, p.nt - c * p.per);
+  const int local = it - before;
+  const int mt = local / cols;
+  TileRef t;
+  t.n0 = (c * p.per + local - mt * cols) * bn;
   if (P.rows.n_groups == nullptr) {
+    t.e = 0;
     t.pos0 = mt * BM;
-    if (t.pos0 >= P.M) return t;
     t.rows = min(BM, P.M - t.pos0);
-    t.valid = 1;
-    return t;
-  }
-  const int ng = ldc(P.rows.n_groups);
-  if (mt >= ldc(P.tile_start + ng)) return t;
-  int lo = 0, hi = ng - 1;  // the group g with tile_start[g] <= mt < tile_start[g + 1]
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (ldc(P.tile_start + mid) <= mt)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  const int g = lo;
-  const int start = ldc(P.rows.group_start + g);
-  const int count = ldc(P.rows.group_start + g + 1) - start;
-  const int local = mt - ldc(P.tile_start + g);
-  t.e = ldc(P.rows.group_expert + g);
-  t.pos0 = start + local * BM;
-  t.rows = min(BM, count - local * BM);
-  t.valid = 1;
-  return t;
-}
-
-// Workgroups of a problem: row tiles rounded up to whole XCD rounds.
-__host__ __device__ inline int grid_of(int mtiles, int ntiles) {
-  return ((mtiles + kXcds - 1) / kXcds) * kXcds * ntiles;
-}
-
-// Raw global data of one K step, per thread.
-template <int BM, WKind W>
-struct StepRegs {
-  static constexpr int kThreads = Geo<BM>::kThreads;
-  static constexpr int kAParts = kThreads / BM;                     // threads per activation row (8)
-  static constexpr int kABytes = BK * 2 / kAParts;                  // 32
-  static constexpr int kBBytes = kBRows * BK * (W == kInt8Rows ? 1 : 2) / kThreads;
-  i32x4 a[kABytes / 16];
-  i32x4 b[kBBytes / 16];
-  float scale;
-};
-
-// Per-thread global cursors of a tile, set up once: the activation row, the
-// weight row (or K-blocked column run) and, for int8, the scale of the
-// thread's piece together with its position inside the quantisation group.
-struct Cursor {
-  const uint16_t* a;
-  const char* b;
-  const float* s;
-  int grem;   // K offset of the piece inside its group (groups wider than a step)
-  int gwrap;  // group width when wider than a step, else never reached
-  int sinc;   // scales per step when a step spans whole groups
-};
-
-template <int BM, WKind W, int NPROJ>
-__device__ __forceinline__ Cursor make_cursor(const GemmProblem& P, const TileRef& t, const uint16_t* a_src) {
-  using S = StepRegs<BM, W>;
-  constexpr int T = S::kThreads;
-  const int tid = (int)threadIdx.x;
-  Cursor c;
-  c.a = a_src;
-  c.s = nullptr;
-  c.grem = 0;
-  c.gwrap = 0x7fffffff;
-  c.sinc = 0;
-  // the projection's pointers, selected without indexing the argument block
-  const void* w0 = P.p[0].w;
-  const void* w1 = NPROJ == 2 ? P.p[1].w : w0;
-  if constexpr (W == kBf16KBlocked) {
-    // K-blocked [K/16][N][16]: 8 blocks x kBRows rows x 32 bytes per step;
-    // thread -> block, consecutive rows (contiguous in memory)
-    constexpr int kRowsPer = kBRows * 8 / T;
-    constexpr int kPerBlock = kBRows / kRowsPer;
-    const int kb = tid / kPerBlock;
-    const int r0 = (tid % kPerBlock) * kRowsPer;
-    const int half = kBRows / NPROJ;
-    const bool second = NPROJ == 2 && r0 >= half;
-    const int n = t.n0 + (NPROJ == 2 ? r0 % half : r0);
-    c.b = (const char*)(second ? w1 : w0) + ((int64_t)kb * P.N + n) * 32;
   } else {
-    constexpr int kParts = T / kBRows;  // threads per weight row
-    const int row = tid / kParts;
-    const int part = tid % kParts;
-    const int half = kBRows / NPROJ;
-    const bool second = NPROJ == 2 && row >= half;
-    const int n = t.n0 + (NPROJ == 2 ? row % half : row);
-    constexpr int kEsz = W == kInt8Rows ? 1 : 2;
-    c.b = (const char*)(second ? w1 : w0) + ((int64_t)t.e * P.N + n) * P.K * kEsz + part * S::kBBytes;
-    if constexpr (W == kInt8Rows) {
-      const float* s0 = P.p[0].s;
-      const float* s1 = NPROJ == 2 ? P.p[1].s : s0;
-      // group widths are multiples of 64 that divide or are multiples of BK
-      const int gsize = P.K / P.groups;
-      const int kk = part * S::kBBytes;
-      c.s = (second ? s1 : s0) + ((int64_t)t.e * P.N + n) * P.groups + kk / gsize;
-      if (gsize <= BK) {
-        c.sinc = BK / gsize;
-      } else {
-        c.gwrap = gsize;
-        c.grem = kk % gsize;
-      }
-    }
+    const int start = ldg(P.rows.group_start + g);
+    const int count = ldg(P.rows.group_start + g + 1) - start;
+    t.e = ldg(P.rows.group_expert + g);
+    t.pos0 = start + mt * BM;
+    t.rows = min(BM, count - mt * BM);
   }
-  return c;
+  return t;
 }
 
 // 16 weight bytes at any alignment (the caller's stack may start anywhere):
@@ -256,83 +233,178 @@ __device__ __forceinline__ i32x4 ld16_any(const char* p) {
   __builtin_memcpy(&v, (const UOCR_GLOBAL char*)p, 16);
   return v;
 }
-
-// Loads one K step at the cursor into registers.  VEC: the weights are
-// 16-byte aligned (one 16-byte load per piece); else each piece is read at
-// whatever alignment it has -- the same bytes either way.
-template <int BM, WKind W, int NPROJ, bool VEC>
-__device__ __forceinline__ void load_step(const Cursor& c, StepRegs<BM, W>& R) {
-  using S = StepRegs<BM, W>;
-#pragma unroll
-  for (int i = 0; i < S::kABytes / 16; ++i) R.a[i] = *(const UOCR_GLOBAL i32x4*)(c.a + 8 * i);
-  constexpr int NB = S::kBBytes / 16;
-#pragma unroll
-  for (int i = 0; i < NB; ++i)
-    R.b[i] = VEC ? *(const UOCR_GLOBAL i32x4*)(c.b + 16 * i) : ld16_any(c.b + 16 * i);
-  if constexpr (W == kInt8Rows) R.scale = ldg(c.s);
+template <bool VEC>
+__device__ __forceinline__ i32x4 ld16w(const char* p) {
+  if constexpr (VEC) return *(const UOCR_GLOBAL i32x4*)p;
+  else return ld16_any(p);
 }
 
-// Moves the cursor one K step on when `more` (else it stays on the last step,
-// whose data a repeated load finds in cache).
+// One K step of one wave's weights, per lane: the 32 k of the lane's column
+// in each block (16-byte pieces), and for int8 the step's scale of each.
 template <WKind W>
-__device__ __forceinline__ void advance(const GemmProblem& P, Cursor& c, bool more) {
-  c.a += more ? BK : 0;
-  if constexpr (W == kBf16KBlocked) {
-    c.b += more ? (int64_t)8 * P.N * 32 : 0;  // the thread's K-block, 8 blocks on
-  } else {
-    c.b += more ? BK * (W == kInt8Rows ? 1 : 2) : 0;
+struct WStep {
+  static constexpr int kPieces = W == kInt8Rows ? 2 : 4;
+  i32x4 v[2][kPieces];
+  float s[2];
+};
+
+// The lane's weight addresses at step 0.
+struct WCursor {
+  const char* p[2];
+  const float* s[2];
+  int64_t step;     // bytes per K step
+  int64_t kblock;   // K-blocked: bytes from one 16-k block to the next
+  float spg_inv;    // int8: BK / group width (steps per group, inverted)
+};
+
+template <WKind W, int NPROJ>
+__device__ __forceinline__ WCursor wcursor(const GemmProblem& P, const TileRef& t, int w, int l) {
+  const int m = l & 31, h = l >> 5;
+  WCursor c;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    // a block past the last column reads the last row; its results are not stored
+    const int row = min(NPROJ == 2 ? t.n0 + 32 * w + m : t.n0 + 64 * w + 32 * b + m, P.N - 1);
+    const char* base = (const char*)(NPROJ == 2 && b == 1 ? P.p[1].w : P.p[0].w);
+    const int64_t wrow = (int64_t)t.e * P.N + row;
     if constexpr (W == kInt8Rows) {
-      const int grem = c.grem + (more ? BK : 0);
-      const bool wrap = grem >= c.gwrap;
-      c.s += (more ? c.sinc : 0) + (wrap ? 1 : 0);
-      c.grem = wrap ? grem - c.gwrap : grem;
+      c.p[b] = base + wrow * P.K + 32 * h;
+      c.s[b] = (NPROJ == 2 && b == 1 ? P.p[1].s : P.p[0].s) + wrow * P.groups;
+    } else if constexpr (W == kBf16Rows) {
+      c.p[b] = base + (wrow * P.K + 32 * h) * 2;
+      c.s[b] = nullptr;
+    } else {
+      c.p[b] = base + ((int64_t)(2 * h) * P.N + row) * 32;  // [K/16][N][16]: k-block 2h of step 0
+      c.s[b] = nullptr;
+    }
+  }
+  c.kblock = (int64_t)P.N * 32;
+  c.step = W == kInt8Rows ? BK : W == kBf16Rows ? 2 * BK : (BK / 16) * c.kblock;
+  c.spg_inv = W == kInt8Rows ? (float)BK * (float)P.groups / (float)P.K : 0.0f;
+  return c;
+}
+
+template <WKind W, bool VEC>
+__device__ __forceinline__ void load_w(const WCursor& c, int k, WStep<W>& o) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const char* q = c.p[b] + (int64_t)k * c.step;
+    if constexpr (W == kBf16KBlocked) {
+      o.v[b][0] = ld16w<VEC>(q);
+      o.v[b][1] = ld16w<VEC>(q + 16);
+      o.v[b][2] = ld16w<VEC>(q + c.kblock);
+      o.v[b][3] = ld16w<VEC>(q + c.kblock + 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < WStep<W>::kPieces; ++i) o.v[b][i] = ld16w<VEC>(q + 16 * i);
+    }
+    if constexpr (W == kInt8Rows) {
+      // the step lies in group k / (steps per group); k < 2^16, so the float
+      // quotient of k + 1/2 truncates to it exactly
+      o.s[b] = ldg(c.s[b] + (int)(((float)k + 0.5f) * c.spg_inv));
     }
   }
 }
 
-template <int BM, WKind W>
-__device__ __forceinline__ void store_step(const StepRegs<BM, W>& R, uint16_t* As, uint16_t* Bs) {
-  using S = StepRegs<BM, W>;
-  constexpr int T = S::kThreads;
-  const int tid = (int)threadIdx.x;
-  {
-    i32x4* dst = (i32x4*)(As + (tid / S::kAParts) * kRow + (tid % S::kAParts) * (S::kABytes / 2));
-#pragma unroll
-    for (int i = 0; i < S::kABytes / 16; ++i) dst[i] = R.a[i];
-  }
-  constexpr int NB = S::kBBytes / 16;
-  if constexpr (W == kBf16KBlocked) {
-    constexpr int kRowsPer = kBRows * 8 / T;
-    constexpr int kPerBlock = kBRows / kRowsPer;
-    const int kb = tid / kPerBlock;
-    const int r0 = (tid % kPerBlock) * kRowsPer;
-#pragma unroll
-    for (int i = 0; i < NB; ++i) *(i32x4*)(Bs + (r0 + i / 2) * kRow + kb * 16 + (i & 1) * 8) = R.b[i];
-  } else if constexpr (W == kBf16Rows) {
-    constexpr int kParts = T / kBRows;
-    const int row = tid / kParts, part = tid % kParts;
-    i32x4* dst = (i32x4*)(Bs + row * kRow + part * (BK / kParts));
-#pragma unroll
-    for (int i = 0; i < NB; ++i) dst[i] = R.b[i];
+// The B fragment of block b for k sub-step `sub` (8 k per lane): int8 weights
+// become bf16_rne(f32(q) * scale), the reference's dequantised values.
+template <WKind W>
+__device__ __forceinline__ bf16x8 wfrag(const WStep<W>& S, int b, int sub) {
+  if constexpr (W == kInt8Rows) {
+    const i32x4 piece = S.v[b][sub >> 1];
+    const int d0 = piece[(sub & 1) * 2], d1 = piece[(sub & 1) * 2 + 1];
+    const float s = S.s[b];
+    i32x4 o;
+    o[0] = (int)pack_bf16x2(i8_to_f32<0>(d0) * s, i8_to_f32<1>(d0) * s);
+    o[1] = (int)pack_bf16x2(i8_to_f32<2>(d0) * s, i8_to_f32<3>(d0) * s);
+    o[2] = (int)pack_bf16x2(i8_to_f32<0>(d1) * s, i8_to_f32<1>(d1) * s);
+    o[3] = (int)pack_bf16x2(i8_to_f32<2>(d1) * s, i8_to_f32<3>(d1) * s);
+    return __builtin_bit_cast(bf16x8, o);
   } else {
-    // int8: 16 weights per piece -> 2 x 16 bytes of bf16
-    constexpr int kParts = T / kBRows;
-    const int row = tid / kParts, part = tid % kParts;
-    i32x4* dst = (i32x4*)(Bs + row * kRow + part * (BK / kParts));
-    const float s = R.scale;
+    return __builtin_bit_cast(bf16x8, S.v[b][sub]);
+  }
+}
+
+// The thread's share of one A step: chunk (tid & 7) of rows (tid >> 3) + 32j.
+template <int BM>
+struct AStep {
+  i32x4 v[BM / 32];
+};
+
+template <int BM>
+__device__ __forceinline__ void load_a(const uint16_t* a, const int (&off)[BM / 32], int k, AStep<BM>& o) {
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      uint32_t o[8];
+  for (int j = 0; j < BM / 32; ++j) o.v[j] = *(const UOCR_GLOBAL i32x4*)(a + off[j] + k * BK);
+}
+
+// The stored position of a row's 16-byte chunk c is c ^ swz(row): any 8
+// consecutive rows, and any 16 (their two 128-byte halves fill a 256-byte
+// bank cycle), put the chunk in different banks.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+template <int BM>
+__device__ __forceinline__ void store_a(const AStep<BM>& o, uint16_t* buf) {
+  const int tid = (int)threadIdx.x;
+  const int r = tid >> 3, c = tid & 7;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int v = R.b[i][d];
-        o[2 * d] = pack_bf16x2(i8_to_f32<0>(v) * s, i8_to_f32<1>(v) * s);
-        o[2 * d + 1] = pack_bf16x2(i8_to_f32<2>(v) * s, i8_to_f32<3>(v) * s);
-      }
-      dst[2 * i] = i32x4{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
-      dst[2 * i + 1] = i32x4{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+  for (int j = 0; j < BM / 32; ++j) *(i32x4*)(buf + (r + 32 * j) * BK + 8 * (c ^ swz(r))) = o.v[j];
+}
+
+// One K step: 4 sub-steps of 16 k, each BM/32 x 2 MFMAs.  The A fragments
+// of sub-step k + 1 are read from LDS before the MFMAs of sub-step k issue.
+template <int BM, WKind W>
+__device__ __forceinline__ void mfma_step(f32x16 (&acc)[BM / 32][2], const uint16_t* As, const WStep<W>& ws, int m,
+                                          int h) {
+  constexpr int MB = BM / 32;
+  const uint16_t* row = As + m * BK;  // row 32i + m has the swizzle of m
+  const int sw = swz(m);
+  bf16x8 a[2][MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) a[0][i] = *(const bf16x8*)(row + 32 * i * BK + 8 * ((4 * h) ^ sw));
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) {
+    if (sub < 3) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        a[(sub + 1) & 1][i] = *(const bf16x8*)(row + 32 * i * BK + 8 * ((4 * h + sub + 1) ^ sw));
+    }
+    const bf16x8 b0 = wfrag<W>(ws, 0, sub);
+    const bf16x8 b1 = wfrag<W>(ws, 1, sub);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub & 1][i], b0, acc[i][0], 0, 0, 0);
+      acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub & 1][i], b1, acc[i][1], 0, 0, 0);
     }
   }
+}
+
+// The per-tile pipeline state: NS steps of weights and of A in flight in
+// registers, the accumulators.
+template <int BM, WKind W>
+struct Pipe {
+  static constexpr int MB = BM / 32;
+  static constexpr int NS = kWStages<W>;
+  WStep<W> ws[NS];
+  AStep<BM> as[NS];
+  f32x16 acc[MB][2];
+};
+
+// Step s = round start + u of the main loop.  Vector loads complete in issue
+// order, so waiting for one load waits for every earlier one: the weights
+// and A of step s + NS are both issued during step s, and every wait targets
+// loads issued NS - 1 or more steps earlier.  The loads' step index is
+// clamped to the last step (re-reading it is harmless), so the loop body has
+// no branches and the compiler's waits stay exact.
+template <int u, int BM, WKind W, bool VEC>
+__device__ __forceinline__ void pipe_step(Pipe<BM, W>& p, const GemmProblem& P, const int (&aoff)[BM / 32],
+                                          const WCursor& cur, uint16_t* lds, int s, int S, int m, int h) {
+  constexpr int NS = Pipe<BM, W>::NS;
+  load_a<BM>(P.a, aoff, min(s + NS, S - 1), p.as[u % NS]);  // as[u % NS] held step s, already in LDS
+  mfma_step<BM, W>(p.acc, lds + (u & 1) * BM * BK, p.ws[u % NS], m, h);
+  load_w<W, VEC>(cur, min(s + NS, S - 1), p.ws[u % NS]);
+  // the other buffer was last read in step s - 1, before the barrier that ended it
+  store_a<BM>(p.as[(u + 1) % NS], lds + ((u + 1) & 1) * BM * BK);
+  lds_barrier();
 }
 
 // silu(g) * u for the prefill epilogue: v_exp_f32 and v_rcp_f32 (within a
@@ -344,105 +416,558 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
-template <int BM, WKind W, int NPROJ, bool VEC>
-__device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds) {
-  using S = StepRegs<BM, W>;
-  uint16_t* As = lds;               // [BM][kRow]
-  uint16_t* Bs = lds + BM * kRow;   // [kBRows][kRow]
-  const int tid = (int)threadIdx.x;
-  const int lane = lane_id();
-  const int w = tid >> 6;
-  const int wm = w / kWN;  // 32-row slice
-  const int wn = w % kWN;  // column slice
-
-  // this thread's activation row (padded rows repeat the last real one)
-  const int a_pos = t.pos0 + min(tid / S::kAParts, t.rows - 1);
-  const int a_row =
-      (P.a_by_token && P.rows.n_groups != nullptr) ? ldg(P.rows.group_rows + a_pos) / P.x_div : a_pos;
-  const uint16_t* a_src = P.a + (int64_t)a_row * P.lda + (tid % S::kAParts) * (S::kABytes / 2);
-  Cursor cur = make_cursor<BM, W, NPROJ>(P, t, a_src);
-
-  f32x16 acc[2];
+// The tile's outputs.  C[i][j] of a 32 x 32 MFMA block sits in lane
+// j + 32 * (i / 4 % 2), register 4 * (i / 8) + i % 4.  Gate/up: h rows in
+// bf16, silu(gate) * up of the two blocks; down: fp32 rows.
+template <int BM, int NPROJ>
+__device__ __forceinline__ void store_tile(const GemmProblem& P, const TileRef& t, const f32x16 (&acc)[BM / 32][2],
+                                           int w, int m, int h) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int ib = 0; ib < BM / 32; ++ib) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[c][i] = 0.0f;
-  // LDS rows of this wave's two 32-column B tiles
-  const int brow0 = NPROJ == 2 ? wn * 32 : wn * 64;
-  const int brow1 = NPROJ == 2 ? kBRows / 2 + wn * 32 : wn * 64 + 32;
-
-  // One K step of raw global data in flight: step ks + 1 is loaded into
-  // registers right after step ks has been stored from them, and lands while
-  // the matrix cores work on step ks (the barriers order LDS only, so they
-  // do not wait for it).
-  S R;
-  const int ksteps = P.K / BK;
-  load_step<BM, W, NPROJ, VEC>(cur, R);
-  advance<W>(P, cur, ksteps > 1);
-  for (int ks = 0; ks < ksteps; ++ks) {
-    if (ks > 0) lds_barrier();
-    store_step<BM, W>(R, As, Bs);
-    if (ks + 1 < ksteps) {
-      load_step<BM, W, NPROJ, VEC>(cur, R);
-      advance<W>(P, cur, ks + 2 < ksteps);
-    }
-    lds_barrier();
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      const int kofs = kk + (lane >> 5) * 8;
-      const bf16x8 a = *(const bf16x8*)(As + (wm * 32 + (lane & 31)) * kRow + kofs);
-      const bf16x8 b0 = *(const bf16x8*)(Bs + (brow0 + (lane & 31)) * kRow + kofs);
-      const bf16x8 b1 = *(const bf16x8*)(Bs + (brow1 + (lane & 31)) * kRow + kofs);
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc[1], 0, 0, 0);
-    }
-  }
-
-  // ---------------- epilogue: C[i][j], lane = j + 32*(i/4 % 2), reg = 4*(i/8) + i%4
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    const int row = wm * 32 + i;
-    if (row >= t.rows) continue;
-    const int64_t orow = (int64_t)(t.pos0 + row);
-    if constexpr (NPROJ == 2) {
-      const int col = t.n0 + wn * 32 + (lane & 31);
-      stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(swiglu_fast(acc[0][r], acc[1][r])));
-    } else {
-      const int col = t.n0 + wn * 64 + (lane & 31);
-      stg(P.outf + orow * P.ldo + col, acc[0][r]);
-      stg(P.outf + orow * P.ldo + col + 32, acc[1][r]);
+    for (int r = 0; r < 16; ++r) {
+      const int row = 32 * ib + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (row >= t.rows) continue;
+      const int64_t orow = (int64_t)(t.pos0 + row);
+      if constexpr (NPROJ == 2) {
+        const int col = t.n0 + 32 * w + m;
+        if (col < P.N) stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(swiglu_fast(acc[ib][0][r], acc[ib][1][r])));
+      } else {
+        const int col = t.n0 + 64 * w + m;
+        if (col < P.N) stg(P.outf + orow * P.ldo + col, acc[ib][0][r]);
+        if (col + 32 < P.N) stg(P.outf + orow * P.ldo + col + 32, acc[ib][1][r]);
+      }
     }
   }
 }
 
-template <int BM, WKind W0, int NP, WKind W1, bool VEC>
-__global__ void __launch_bounds__(Geo<BM>::kThreads) k_gemm_pair(GemmProblem a, GemmProblem b, int split) {
-  extern __shared__ uint16_t lds[];
-  constexpr int bn = kBRows / NP;
-  const int wg = (int)blockIdx.x;
-  if (wg < split) {
-    const TileRef t = locate<BM>(a, wg, bn);
-    if (!t.valid) return;
-    gemm_tile<BM, W0, NP, VEC>(a, t, lds);
-  } else {
-    const TileRef t = locate<BM>(b, wg - split, bn);
-    if (!t.valid) return;
-    gemm_tile<BM, W1, NP, VEC>(b, t, lds);
+template <int BM, WKind W, int NPROJ, bool VEC>
+__device__ void gemm_tile(const GemmProblem& P, const TileRef& t, uint16_t* lds) {
+  constexpr int MB = BM / 32;
+  constexpr int NS = kWStages<W>;
+  const int tid = (int)threadIdx.x;
+  const int l = lane_id();
+  const int w = tid >> 6;
+  const int m = l & 31, h = l >> 5;
+  const int S = P.K / BK;
+
+  // this thread's A rows (padded rows repeat the last real one)
+  int aoff[MB];
+#pragma unroll
+  for (int j = 0; j < MB; ++j) {
+    const int pos = t.pos0 + min((tid >> 3) + 32 * j, t.rows - 1);
+    const int row = (P.a_by_token && P.rows.n_groups != nullptr) ? ldg(P.rows.group_rows + pos) / P.x_div : pos;
+    aoff[j] = (int)((int64_t)row * P.lda) + 8 * (tid & 7);
   }
+  const WCursor cur = wcursor<W, NPROJ>(P, t, w, l);
+
+  Pipe<BM, W> p;
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p.acc[i][0][r] = p.acc[i][1][r] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    load_a<BM>(P.a, aoff, min(i, S - 1), p.as[i]);
+    load_w<W, VEC>(cur, min(i, S - 1), p.ws[i]);
+  }
+  store_a<BM>(p.as[0], lds);
+  lds_barrier();
+  // S is even (K is a multiple of 2 * BK): full rounds of NS steps, then the
+  // remaining S % NS (0 or 2) steps, whose data the last round loaded
+  const int rounds = S / NS;
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int s = rd * NS;
+    pipe_step<0, BM, W, VEC>(p, P, aoff, cur, lds, s, S, m, h);
+    pipe_step<1, BM, W, VEC>(p, P, aoff, cur, lds, s + 1, S, m, h);
+    if constexpr (NS == 4) {
+      pipe_step<2, BM, W, VEC>(p, P, aoff, cur, lds, s + 2, S, m, h);
+      pipe_step<3, BM, W, VEC>(p, P, aoff, cur, lds, s + 3, S, m, h);
+    }
+  }
+  if (NS == 4 && rounds * NS < S) {
+    // the tail's steps are rounds * 4 + {0, 1}: weights in ws[0], ws[1]; A in buffer 0 and in as[1]
+    mfma_step<BM, W>(p.acc, lds, p.ws[0], m, h);
+    store_a<BM>(p.as[1], lds + BM * BK);
+    lds_barrier();
+    mfma_step<BM, W>(p.acc, lds + BM * BK, p.ws[1], m, h);
+    lds_barrier();
+  }
+  store_tile<BM, NPROJ>(P, t, p.acc, w, m, h);
+}
+
+// The routed problem `a` (weights W0) and the shared experts' `b` (K-blocked
+// bf16) in one persistent launch: each XCD's workgroups walk that XCD's tiles
+// of a, then of b.
+template <int BM, WKind W0, int NP, bool VEC>
+__global__ void __launch_bounds__(kGThreads) k_moe_gemm(GemmProblem a, GemmProblem b) {
+  extern __shared__ uint16_t lds[];
+  constexpr int bn = kWRowsWg / NP;
+  const int x = (int)blockIdx.x % kXcds;
+  const int j = (int)blockIdx.x / kXcds;
+  const int J = (int)gridDim.x / kXcds;
+  const Plan pa = plan_of(a, bn);
+  const Plan pb = plan_of(b, bn);
+  const int fa = xcd_prefix<BM>(a, pa, x);
+  const int fb = xcd_prefix<BM>(b, pb, x);
+  const int na = __builtin_amdgcn_readlane(fa, kWave - 1);
+  const int nb = __builtin_amdgcn_readlane(fb, kWave - 1);
+  for (int it = j; it < na + nb; it += J) {
+    if (it < na)
+      gemm_tile<BM, W0, NP, VEC>(a, tile_at<BM>(a, pa, x, fa, it, bn), lds);
+    else
+      gemm_tile<BM, kBf16KBlocked, NP, VEC>(b, tile_at<BM>(b, pb, x, fb, it - na, bn), lds);
+  }
+}
+
+// Workgroups of the persistent grid: every CU's resident share, a whole
+// number per XCD.
+template <int BM, WKind W0, int NP, bool VEC>
+hipError_t moe_gemm_grid(int* grid) {
+  static std::atomic<int> cached{0};
+  int g = cached.load(std::memory_order_relaxed);
+  if (g == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_gemm<BM, W0, NP, VEC>, kGThreads,
+                                                       (size_t)2 * BM * BK * sizeof(uint16_t));
+    if (e != hipSuccess) return e;
+    g = (cus / kXcds > 0 ? cus / kXcds : 1) * (per_cu > 0 ? per_cu : 1) * kXcds;
+    cached.store(g, std::memory_order_relaxed);
+  }
+  *grid = g;
+  return hipSuccess;
 }
 
 template <int BM, WKind W0, int NP, bool VEC = true>
-hipError_t launch_pair_bm(const GemmProblem& routed, const GemmProblem& shared, int max_mtiles, hipStream_t s,
-                          const char* name) {
-  constexpr int bn = kBRows / NP;
-  const int split = grid_of(max_mtiles, routed.N / bn);
-  const int shared_wgs = grid_of((shared.M + BM - 1) / BM, shared.N / bn);
-  const int wgs = split + shared_wgs;
-  if (wgs == 0) return hipSuccess;
-  const size_t lds = (size_t)(BM + kBRows) * kRow * sizeof(uint16_t);
-  UOCR_LAUNCH(name, (k_gemm_pair<BM, W0, NP, kBf16KBlocked, VEC>), dim3(wgs), dim3(Geo<BM>::kThreads), lds, s, routed,
-              shared, split);
+hipError_t launch_moe_gemm(const GemmProblem& routed, const GemmProblem& shared, hipStream_t s, const char* name) {
+  int grid = 0;
+  const hipError_t e = moe_gemm_grid<BM, W0, NP, VEC>(&grid);
+  if (e != hipSuccess) return e;
+  UOCR_LAUNCH(name, (k_moe_gemm<BM, W0, NP, VEC>), dim3(grid), dim3(kGThreads), (size_t)2 * BM * BK * sizeof(uint16_t),
+              s, routed, shared);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------- LDS-staged path
+//
+// The same tiles and placement for 16-byte aligned operands, with every
+// operand streamed into LDS by global_load_lds_dwordx4 (lane l of a wave
+// writes its 16 bytes at the instruction's LDS address + 16 l), so no
+// registers hold data in flight: with 64-row tiles two workgroups share a CU
+// and one's MFMAs overlap the other's dequantisation (the int8 path's VALU
+// work, about ten VALU instructions per MFMA, bounds a lone wave).  A step is
+// 64 k: every weight row contributes 64 (int8) or 128 (bf16) contiguous bytes,
+// 4 or 8 lanes to a row, where the fragment-layout loads touch 32 rows per
+// instruction.  A stage holds the workgroup's 256 weight rows, the A step and
+// (int8) the step's scale of every weight row; kCount stages form a ring,
+// each loaded kCount - 1 steps ahead.  Each wave loads exactly the weight
+// rows and scales it reads, so only the shared A step needs the barrier.  The
+// waits are explicit (s_waitcnt vmcnt(n) before the barrier, n the loads
+// issued since the step's own): every thread issues the same number of loads
+// per step, the loads past the last step re-read it, and no other vector
+// memory access happens inside the K loop.  Lane half h covers k = 32h ..
+// 32h + 31 of a step, as in the fragment-load path, so both give the same bits.
+
+// Rows per tile of the LDS-staged path: 128 for int8 weights (each
+// dequantised weight feeds up to four 32-row MFMA blocks; blocks past a
+// tile's rows are skipped), 64 for bf16 weights, whose 128-byte weight rows
+// leave room for two stages of 64-row A steps only.
+template <WKind W>
+constexpr int kLdsBM = W == kInt8Rows ? 128 : 64;
+constexpr int kWgPerCu = 2;  // two workgroups share a CU: one's barrier waits overlap the other's work
+
+template <int BM, WKind W>
+struct Stage {
+  static constexpr int kBRowBytes = W == kInt8Rows ? BK : 2 * BK;  // one step of a weight row
+  static constexpr int kBBytes = kWRowsWg * kBRowBytes;
+  static constexpr int kABytes = BM * 2 * BK;
+  static constexpr int kSBytes = W == kInt8Rows ? kWRowsWg * 4 : 0;
+  static constexpr int kBytes = kBBytes + kABytes + kSBytes;
+  static constexpr int kBudget = 160 * 1024 / kWgPerCu;
+  static constexpr int kCount = kBudget / kBytes < 4 ? kBudget / kBytes : 4;
+  static constexpr int kBLoads = kBBytes / 1024 / 4;           // weight loads per thread per step
+  static constexpr int kALoads = kABytes / 16 / kGThreads;      // A loads per thread per step
+  static constexpr int kLoads = kBLoads + kALoads + (W == kInt8Rows ? 1 : 0);
+  static_assert(kCount >= 2, "two stages");
+};
+
+template <WKind W>
+constexpr int kRing = Stage<kLdsBM<W>, W>::kBytes * Stage<kLdsBM<W>, W>::kCount;
+template <WKind W0>
+constexpr int kLdsBytes = kRing<W0> > kRing<kBf16KBlocked> ? kRing<W0> : kRing<kBf16KBlocked>;
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+__device__ __forceinline__ void dma16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds((const UOCR_GLOBAL void*)g, (lds_ptr)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds((const UOCR_GLOBAL void*)g, (lds_ptr)l, 4, 0, 0);
+}
+
+// This thread's loads of the step N loads back have landed, then the barrier:
+// after it every wave's loads of that step are in LDS and every wave has
+// finished reading the previous step.
+template <int N>
+__device__ __forceinline__ void step_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Stored position of chunk c of a 64-byte int8 weight row r: c ^ swz64(r).
+// Any 8 consecutive rows (128-byte bank cycle) and any 16 (256-byte cycle)
+// put a chunk in different banks.
+__device__ __forceinline__ int swz64(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+// One step from a stage: 4 MFMA sub-steps, lane half h at k = 32h + 8 sub.
+// The wave's weight bytes of the step are read first, and the A fragments of
+// sub-step k + 1 before the MFMAs of sub-step k.
+template <int BM, WKind W>
+__device__ __forceinline__ void lds_step(f32x16 (&acc)[BM / 32][2], const char* st, int w, int m, int h,
+                                         int nact) {
+  using St = Stage<BM, W>;
+  constexpr int MB = BM / 32;
+  constexpr int RB = St::kBRowBytes;
+  constexpr int NQ = W == kInt8Rows ? 2 : 4;  // the lane's 16-byte weight chunks per block
+  const char* Bw = st + 64 * w * RB;          // the wave's 64 weight rows
+  const char* A = st + St::kBBytes;
+  const int sw = swz(m);  // 128-byte rows 32i + m (A, bf16 weights)
+  i32x4 raw[2][NQ];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c = NQ * h + q;
+      if constexpr (W == kBf16KBlocked) {
+        // [4 k-blocks][256 rows][32 bytes], the two 16-byte halves of rows 8..15 of
+        // every 16 swapped: k-block c / 2 of the step, half c % 2
+        raw[b][q] = *(const i32x4*)(st + ((c >> 1) * kWRowsWg + 64 * w + 32 * b + m) * 32 +
+                                    16 * ((c & 1) ^ ((m >> 3) & 1)));
+      } else {
+        raw[b][q] = *(const i32x4*)(Bw + (32 * b + m) * RB + 16 * (c ^ (W == kInt8Rows ? swz64(m) : sw)));
+      }
+    }
+  float sc[2] = {1.0f, 1.0f};
+  if constexpr (W == kInt8Rows) {
+    const float* S = (const float*)(st + St::kBBytes + St::kABytes);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) sc[b] = S[64 * w + 32 * b + m];
+  }
+  // 32-row blocks past the tile's rows (nact of them hold rows) are skipped.
+  // 64-row tiles read the A fragments of sub-step k + 1 during sub-step k;
+  // 128-row tiles read each sub-step's own (registers for two waves a SIMD),
+  // the other workgroup on the CU covering the wait.
+  constexpr int AB = MB > 2 ? 1 : 2;
+  bf16x8 a[AB][MB];
+  auto read_a = [&](bf16x8(&dst)[MB], int sub) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+      if (i < nact) dst[i] = *(const bf16x8*)(A + (32 * i + m) * 2 * BK + 16 * ((4 * h + sub) ^ sw));
+  };
+  if constexpr (AB == 2) read_a(a[0], 0);
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) {
+    if constexpr (AB == 2) {
+      if (sub < 3) read_a(a[(sub + 1) & 1], sub + 1);
+    } else {
+      read_a(a[0], sub);
+    }
+    bf16x8 bf[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if constexpr (W == kInt8Rows) {
+        const int d0 = raw[b][sub >> 1][(sub & 1) * 2], d1 = raw[b][sub >> 1][(sub & 1) * 2 + 1];
+        i32x4 o;
+        o[0] = (int)pack_bf16x2(i8_to_f32<0>(d0) * sc[b], i8_to_f32<1>(d0) * sc[b]);
+        o[1] = (int)pack_bf16x2(i8_to_f32<2>(d0) * sc[b], i8_to_f32<3>(d0) * sc[b]);
+        o[2] = (int)pack_bf16x2(i8_to_f32<0>(d1) * sc[b], i8_to_f32<1>(d1) * sc[b]);
+        o[3] = (int)pack_bf16x2(i8_to_f32<2>(d1) * sc[b], i8_to_f32<3>(d1) * sc[b]);
+        bf[b] = __builtin_bit_cast(bf16x8, o);
+      } else {
+        bf[b] = __builtin_bit_cast(bf16x8, raw[b][sub]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (i < nact) {
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[0], acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[1], acc[i][1], 0, 0, 0);
+      }
+    }
+    // keep each sub-step's dequantisation next to its MFMAs (the two issue in
+    // turn on a SIMD anyway): hoisting it only lengthens register lifetimes
+    if constexpr (MB > 2) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int BM, WKind W, int NPROJ>
+__device__ void lds_tile(const GemmProblem& P, const TileRef& t, char* lds) {
+  using St = Stage<BM, W>;
+  constexpr int NS = St::kCount, NB = St::kBLoads, NA = St::kALoads;
+  constexpr int RB = St::kBRowBytes;
+  constexpr int RPL = 1024 / RB;  // weight rows per load
+  const int tid = (int)threadIdx.x;
+  const int j = lane_id();
+  const int w = tid >> 6;
+  const int m = j & 31, h = j >> 5;
+  const int S = P.K / BK;
+
+  // weight rows: load i of the step fills stage rows 64w + RPL i + j / (RB / 16),
+  // stored chunk j % (RB / 16) holding chunk (stored) ^ swizzle(row)
+  const char* bsrc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if constexpr (W == kBf16KBlocked) {
+      // load i: k-block i / 2 of the step for rows 32 (i % 2) .. + 31 of the wave's 64,
+      // 1 KB contiguous in [K/16][N][16]; lane j holds half (j % 2) ^ (row bit 3) of row j / 2
+      const int b = i & 1;
+      const int lr = j >> 1;
+      const int row = min(NPROJ == 2 ? t.n0 + 32 * w + lr : t.n0 + 64 * w + 32 * b + lr, P.N - 1);
+      const int hf = (j & 1) ^ ((lr >> 3) & 1);
+      const char* base = (const char*)(NPROJ == 2 && b == 1 ? P.p[1].w : P.p[0].w);
+      bsrc[i] = base + ((int64_t)(i >> 1) * P.N + row) * 32 + 16 * hf;
+      continue;
+    }
+    const int rr = RPL * i + j / (RB / 16);  // row within the wave's 64
+    const int b = rr >> 5;
+    const int mm = rr & 31;
+    const int row = min(NPROJ == 2 ? t.n0 + 32 * w + mm : t.n0 + 64 * w + rr, P.N - 1);
+    const int c = (j % (RB / 16)) ^ (W == kInt8Rows ? swz64(rr) : swz(rr));
+    const char* base = (const char*)(NPROJ == 2 && b == 1 ? P.p[1].w : P.p[0].w);
+    const int64_t wrow = (int64_t)t.e * P.N + row;
+    if constexpr (W == kInt8Rows)
+      bsrc[i] = base + wrow * P.K + 16 * c;
+    else
+      bsrc[i] = base + wrow * P.K * 2 + 16 * c;
+  }
+  const int64_t bstep = W == kBf16KBlocked ? (int64_t)(BK / 16) * P.N * 32 : RB;
+
+  // A: load i of the step fills chunk j % 8 of stage row (64 (w NA + i) + j) / 8
+  int aoff[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int r = ((w * NA + i) * 64 + j) >> 3;
+    const int c = (j & 7) ^ swz(r);
+    const int pos = t.pos0 + min(r, t.rows - 1);
+    const int row = (P.a_by_token && P.rows.n_groups != nullptr) ? ldg(P.rows.group_rows + pos) / P.x_div : pos;
+    aoff[i] = (int)((int64_t)row * P.lda) + 8 * c;
+  }
+
+  // int8 scales: lane j of wave w loads the scale of stage row 64w + j
+  const float* ssrc = nullptr;
+  float ginv = 0.0f;
+  if constexpr (W == kInt8Rows) {
+    const int b = j >> 5;
+    const int row = min(NPROJ == 2 ? t.n0 + 32 * w + m : t.n0 + 64 * w + j, P.N - 1);
+    ssrc = (NPROJ == 2 && b == 1 ? P.p[1].s : P.p[0].s) + ((int64_t)t.e * P.N + row) * P.groups;
+    ginv = (float)P.groups / (float)P.K;  // 1 / group width
+  }
+
+  // the loads of step s (clamped to the last step) into stage s % NS
+  auto issue = [&](int s) {
+    const int sc = min(s, S - 1);
+    char* st = lds + (s % NS) * St::kBytes;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if constexpr (W == kBf16KBlocked)
+        dma16(bsrc[i] + sc * bstep, st + ((i >> 1) * kWRowsWg + 64 * w + 32 * (i & 1)) * 32);
+      else
+        dma16(bsrc[i] + sc * bstep, st + (64 * w + RPL * i) * RB);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) dma16(P.a + aoff[i] + sc * BK, st + St::kBBytes + (w * NA + i) * 1024);
+    if constexpr (W == kInt8Rows) {
+      // the group of the step's k (k < 2^16: the float quotient of k + 1/2 truncates to it exactly)
+      const int g = (int)(((float)(sc * BK) + 0.5f) * ginv);
+      dma4(ssrc + g, st + St::kBBytes + St::kABytes + 64 * w * 4);
+    }
+  };
+
+  f32x16 acc[BM / 32][2];
+#pragma unroll
+  for (int i = 0; i < BM / 32; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][0][r] = acc[i][1][r] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i) issue(i);
+  const int nact = __builtin_amdgcn_readfirstlane((t.rows + 31) >> 5);
+  for (int s = 0; s < S; ++s) {
+    step_barrier<(NS - 2) * St::kLoads>();
+    issue(s + NS - 1);  // into the stage read in step s - 1, which every wave has finished
+    lds_step<BM, W>(acc, lds + (s % NS) * St::kBytes, w, m, h, nact);
+  }
+  // every wave has finished reading the stages before the next tile's loads
+  step_barrier<(NS - 1) * St::kLoads>();
+  store_tile<BM, NPROJ>(P, t, acc, w, m, h);
+}
+
+// Balanced placement for the LDS-staged path.  The tiles of a range (row
+// tile major) are cut into pieces of about total / (8 kPiecesPerXcd) tiles,
+// whole row tiles each, and the pieces are dealt round robin to the XCDs in
+// range order, so each XCD's share is within one piece of the mean while a
+// piece's row tiles still share their weight tiles in one L2.  Every wave
+// plans for its XCD with a 128-int scratch of its own in LDS.
+constexpr int kPiecesPerXcd = 8;
+
+struct Pieces {
+  int prefix;  // lane v: inclusive prefix of the tile counts of the XCD's pieces 0..v
+  int rk;      // lane v: range << 16 | index of the piece within its range
+  int q;       // tiles per piece (target)
+  int total;   // pieces of the problem
+};
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ int wave_scan_i(int v) {  // inclusive
+  const int l = lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int u = __shfl_up(v, off, kWave);
+    if (l >= off) v += u;
+  }
+  return v;
+}
+
+// Pieces of problem P for XCD x, dealt from XCD u0 on (piece u of the problem
+// to XCD (u0 + u) % 8); at most 128 ranges and 512 pieces.
+template <int BM>
+__device__ Pieces plan_pieces(const GemmProblem& P, const Plan& p, int x, int u0, int* sc) {
+  const int l = lane_id();
+  const int R = p.ng * p.nr;
+  int items[2], tiles[2], cols[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int r = l + 64 * hh;
+    items[hh] = tiles[hh] = 0;
+    cols[hh] = 1;
+    if (r < R) {
+      const int g = r / p.nr;
+      const int c = r - g * p.nr;
+      cols[hh] = min(p.per, p.nt - c * p.per);
+      tiles[hh] = row_tiles<BM>(P, g);
+      items[hh] = tiles[hh] * cols[hh];
+    }
+  }
+  const int total = wave_sum_i(items[0] + items[1]);
+  const int q = max(1, (total + kXcds * kPiecesPerXcd - 1) / (kXcds * kPiecesPerXcd));
+  int np[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int pr = max(1, (q + cols[hh] - 1) / cols[hh]);  // row tiles per piece
+    np[hh] = (tiles[hh] + pr - 1) / pr;
+  }
+  const int inc0 = wave_scan_i(np[0]);
+  const int tot0 = __builtin_amdgcn_readlane(inc0, kWave - 1);
+  const int inc1 = wave_scan_i(np[1]) + tot0;
+  const int totp = __builtin_amdgcn_readlane(inc1, kWave - 1);
+  sc[l] = inc0 - np[0];  // first piece of range l
+  sc[64 + l] = inc1 - np[1];
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own stores, before it reads them
+  // this lane's piece: the v-th of XCD x
+  const int xs = (x - u0 % kXcds + kXcds) % kXcds;
+  const int u = xs + kXcds * l;
+  int it = 0, rk = 0;
+  if (u < totp) {
+    int lo = 0, hi = R - 1;  // the last range whose first piece is <= u (every range has a piece)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (sc[mid] <= u)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int r = lo;
+    const int k = u - sc[r];
+    const int g = r / p.nr;
+    const int c = r - g * p.nr;
+    const int cl = min(p.per, p.nt - c * p.per);
+    const int pr = max(1, (q + cl - 1) / cl);
+    const int rows = min(pr, row_tiles<BM>(P, g) - k * pr);
+    it = rows * cl;
+    rk = (r << 16) | k;
+  }
+  return Pieces{wave_scan_i(it), rk, q, totp};
+}
+
+// Tile `it` of the XCD's pieces.
+template <int BM>
+__device__ TileRef piece_tile(const GemmProblem& P, const Plan& p, const Pieces& pc, int it, int bn) {
+  const int v = (int)__popcll(__ballot(pc.prefix <= it));
+  const int before = v > 0 ? __builtin_amdgcn_readlane(pc.prefix, v - 1) : 0;
+  const int rk = __builtin_amdgcn_readlane(pc.rk, v);
+  const int r = rk >> 16, k = rk & 0xffff;
+  const int g = r / p.nr;
+  const int c = r - g * p.nr;
+  const int cols = min(p.per, p.nt - c * p.per);
+  const int pr = max(1, (pc.q + cols - 1) / cols);
+  const int local = it - before;
+  const int mt = k * pr + local / cols;
+  TileRef t;
+  t.n0 = (c * p.per + local % cols) * bn;
+  if (P.rows.n_groups == nullptr) {
+    t.e = 0;
+    t.pos0 = mt * BM;
+    t.rows = min(BM, P.M - t.pos0);
+  } else {
+    const int start = ldg(P.rows.group_start + g);
+    const int count = ldg(P.rows.group_start + g + 1) - start;
+    t.e = ldg(P.rows.group_expert + g);
+    t.pos0 = start + mt * BM;
+    t.rows = min(BM, count - mt * BM);
+  }
+  return t;
+}
+
+template <WKind W0, int NP>
+__global__ void __launch_bounds__(kGThreads, kWgPerCu) k_moe_gemm_lds(GemmProblem a, GemmProblem b) {
+  extern __shared__ __attribute__((aligned(16))) char lds_stages[];
+  constexpr int bn = kWRowsWg / NP;
+  constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
+  const int x = (int)blockIdx.x % kXcds;
+  const int j = (int)blockIdx.x / kXcds;
+  const int J = (int)gridDim.x / kXcds;
+  const Plan pa = plan_of(a, bn);
+  const Plan pb = plan_of(b, bn);
+  // each wave plans in its own 512 bytes of the (not yet used) stage ring
+  int* sc = (int*)lds_stages + (threadIdx.x >> 6) * 128;
+  const Pieces qa = plan_pieces<BMA>(a, pa, x, 0, sc);
+  const Pieces qb = plan_pieces<BMB>(b, pb, x, qa.total, sc);  // dealt on from where a's ended
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave done with its scratch
+  const int na = __builtin_amdgcn_readlane(qa.prefix, kWave - 1);
+  const int nb = __builtin_amdgcn_readlane(qb.prefix, kWave - 1);
+  for (int it = j; it < na + nb; it += J) {
+    if (it < na)
+      lds_tile<BMA, W0, NP>(a, piece_tile<BMA>(a, pa, qa, it, bn), lds_stages);
+    else
+      lds_tile<BMB, kBf16KBlocked, NP>(b, piece_tile<BMB>(b, pb, qb, it - na, bn), lds_stages);
+  }
+}
+
+template <WKind W0, int NP>
+hipError_t launch_moe_gemm_lds(const GemmProblem& routed, const GemmProblem& shared, hipStream_t s,
+                               const char* name) {
+  constexpr size_t lds = kLdsBytes<W0>;
+  static std::atomic<int> cached{0};
+  int grid = cached.load(std::memory_order_relaxed);
+  if (grid == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)k_moe_gemm_lds<W0, NP>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_gemm_lds<W0, NP>, kGThreads, lds);
+    if (e != hipSuccess) return e;
+    grid = (cus / kXcds > 0 ? cus / kXcds : 1) * (per_cu > 0 ? per_cu : 1) * kXcds;
+    cached.store(grid, std::memory_order_relaxed);
+  }
+  UOCR_LAUNCH(name, (k_moe_gemm_lds<W0, NP>), dim3(grid), dim3(kGThreads), lds, s, routed, shared);
   return hipGetLastError();
 }
 
@@ -466,32 +991,29 @@ hipError_t launch_quantize(int8_t* q, float* scales, const void* w, int w_bf16, 
   return hipGetLastError();
 }
 
-int gemm_bk() { return BK; }
+// K granularity of the grouped GEMM: two steps.
+int gemm_bk() { return 2 * BK; }
 
-hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
-                            hipStream_t s, bool vec) {
+hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, hipStream_t s, bool vec) {
   const bool gu = routed.swiglu != 0;
   const char* name = gu ? "gemm_gateup" : "gemm_down";
+  if (routed.N % 32 || shared.N % 32 || routed.K % (2 * BK) || shared.K % (2 * BK)) return hipErrorInvalidValue;
+  if (routed.kind == kInt8Rows && (routed.K % routed.groups || (routed.K / routed.groups) % BK))
+    return hipErrorInvalidValue;
   if (!vec) {  // weights at any alignment: 64-row tiles only
     if (bm != 64) return hipErrorInvalidValue;
     if (routed.kind == kInt8Rows)
-      return gu ? launch_pair_bm<64, kInt8Rows, 2, false>(routed, shared, max_mtiles, s, name)
-                : launch_pair_bm<64, kInt8Rows, 1, false>(routed, shared, max_mtiles, s, name);
-    return gu ? launch_pair_bm<64, kBf16Rows, 2, false>(routed, shared, max_mtiles, s, name)
-              : launch_pair_bm<64, kBf16Rows, 1, false>(routed, shared, max_mtiles, s, name);
+      return gu ? launch_moe_gemm<64, kInt8Rows, 2, false>(routed, shared, s, name)
+                : launch_moe_gemm<64, kInt8Rows, 1, false>(routed, shared, s, name);
+    return gu ? launch_moe_gemm<64, kBf16Rows, 2, false>(routed, shared, s, name)
+              : launch_moe_gemm<64, kBf16Rows, 1, false>(routed, shared, s, name);
   }
-  if (bm == 128) {
-    if (routed.kind == kInt8Rows)
-      return gu ? launch_pair_bm<128, kInt8Rows, 2>(routed, shared, max_mtiles, s, name)
-                : launch_pair_bm<128, kInt8Rows, 1>(routed, shared, max_mtiles, s, name);
-    return gu ? launch_pair_bm<128, kBf16Rows, 2>(routed, shared, max_mtiles, s, name)
-              : launch_pair_bm<128, kBf16Rows, 1>(routed, shared, max_mtiles, s, name);
-  }
+  // 16-byte aligned operands: the LDS-staged kernel (its tile heights are its own)
   if (routed.kind == kInt8Rows)
-    return gu ? launch_pair_bm<64, kInt8Rows, 2>(routed, shared, max_mtiles, s, name)
-              : launch_pair_bm<64, kInt8Rows, 1>(routed, shared, max_mtiles, s, name);
-  return gu ? launch_pair_bm<64, kBf16Rows, 2>(routed, shared, max_mtiles, s, name)
-            : launch_pair_bm<64, kBf16Rows, 1>(routed, shared, max_mtiles, s, name);
+    return gu ? launch_moe_gemm_lds<kInt8Rows, 2>(routed, shared, s, name)
+              : launch_moe_gemm_lds<kInt8Rows, 1>(routed, shared, s, name);
+  return gu ? launch_moe_gemm_lds<kBf16Rows, 2>(routed, shared, s, name)
+            : launch_moe_gemm_lds<kBf16Rows, 1>(routed, shared, s, name);
 }
 
 }  // namespace uocr

@@ -164,11 +164,12 @@ struct GemmProblem {
   int64_t ldo;
   int out_by_position;        // 1: output row = position in group order, 0: row id
 };
-// bm: rows per tile, 64 or 128 (must match the group tables' tile_start).
-// vec: every weight pointer is 16-byte aligned; else the weights are read at
-// any alignment (bm must be 64), with the same bits.
-hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, int max_mtiles,
-                            hipStream_t s, bool vec = true);
+// bm: rows per tile, 64 or 128.  vec: every weight pointer is 16-byte
+// aligned; else the weights are read at any alignment (bm must be 64), with
+// the same bits.  N must be a multiple of 32 and K of 128 (and of the int8
+// group, itself a multiple of 64); a routed problem has at most 64 groups.
+hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, hipStream_t s,
+                            bool vec = true);
 
 // ---- the n-gram logit guard (ngram.hip) ----
 

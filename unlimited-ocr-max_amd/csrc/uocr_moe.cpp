@@ -1150,7 +1150,6 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   }
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
   const int max_groups = (int)(E < R ? E : R);
-  const int max_mtiles = (int)((R + BM - 1) / BM) + max_groups;
 
   GemmProblem gu{};
   gu.a = d.xb;
@@ -1186,7 +1185,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sgu.swiglu = 1;
   sgu.outb = d.hsb;
   sgu.ldo = Fs;
-  e = launch_gemm_pair(gu, sgu, BM, max_mtiles, s, vec);
+  e = launch_gemm_pair(gu, sgu, BM, s, vec);
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
 
   GemmProblem dn = gu;
@@ -1216,7 +1215,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sdn.outb = nullptr;
   sdn.outf = d.sh;
   sdn.ldo = H;
-  e = launch_gemm_pair(dn, sdn, BM, max_mtiles, s, vec);
+  e = launch_gemm_pair(dn, sdn, BM, s, vec);
   if (e == hipSuccess) e = launch_combine(out, d.y, H, d.wts, d.g.inv, d.sh, (int)T, H, (int)L->top_k, s);
   if (e == hipSuccess && expert_ids) e = hipMemcpyAsync(expert_ids, d.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
   if (e == hipSuccess && expert_weights)
