@@ -310,7 +310,7 @@ __device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) {
 // sum, divide; the k largest probabilities in turn, ties to the lower id),
 // then one more on the workgroup's count of routed tokens.
 __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int t, uint32_t tag, int* r_ids,
-                                                           float* r_wts, int* r_done) {
+                                                           float* r_wts, int* r_done, uint64_t* keys) {
   const int l = lane();
   const uint64_t* src = A.logits + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
   uint64_t q;
@@ -329,30 +329,36 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   const float S = tree_sum(ex);
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 4] = (int64_t)wall_clock64();
   const float pr = real ? ex / S : 0.0f;
-  bool cand = real;
-  float d = 0.0f;
-  int my_sel = 0;      // lane j < topk: the j-th selection
-  float my_w = 0.0f;
-  for (int j = 0; j < A.topk; ++j) {
-    const uint32_t bits = cand ? __float_as_uint(pr) : 0u;
-    const uint32_t best = tree_umax(bits);
-    const int sel = (int)__builtin_ctzll(__ballot(cand && bits == best));
-    const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr), sel));
-    d = d + ws;
-    cand = cand && l != sel;
-    if (l == j) {
-      my_sel = sel;
-      my_w = ws;
-    }
+  // The k largest probabilities in turn, ties to the lower id, as ranks: lane
+  // l's key ((bits of pr) << 6 | 63 - l) + 1 (0 past the experts) is distinct
+  // and orders lanes exactly that way, so the j-th selection is the lane with
+  // j larger keys.  Every lane counts them over the 64 keys in LDS (independent
+  // compares, where selecting in turn is six dependent wave reductions).
+  const uint64_t key = real ? ((((uint64_t)__float_as_uint(pr)) << 6) | (uint64_t)(63 - l)) + 1ull : 0ull;
+  keys[l] = key;
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < kWave; j += 2) {
+    const u64x2 kk = *(const u64x2*)(keys + j);
+    rank += (kk[0] > key ? 1 : 0) + (kk[1] > key ? 1 : 0);
+  }
+  const bool chosen = real && rank < A.topk;
+  float my_w = pr;
+  if (A.renorm) {
+    // the selected probabilities summed in selection order, then divided
+    float* ws = (float*)(keys + kWave);
+    if (chosen) ws[rank] = pr;
+    float d = 0.0f;
+    for (int j = 0; j < A.topk; ++j) d = d + ws[j];
+    my_w = pr / d;
   }
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 5] = (int64_t)wall_clock64();
-  if (A.renorm) my_w = my_w / d;
-  if (l < A.topk) {
-    const int i = t * A.topk + l;
-    r_ids[i] = my_sel;
+  if (chosen) {
+    const int i = t * A.topk + rank;
+    r_ids[i] = l;
     r_wts[i] = my_w;
     if (blockIdx.x == 0) {
-      if (A.ids_out != nullptr) A.ids_out[i] = my_sel;
+      if (A.ids_out != nullptr) A.ids_out[i] = l;
       if (A.wts_out != nullptr) A.wts_out[i] = my_w;
     }
   }
@@ -921,7 +927,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   // tasks come late in the list); the other waves meanwhile run their tasks
   // that do not need the routing (the shared experts).
   const int rwave = kWaves - 1 - wave;
-  if (rwave < A.B) route_token(A, rwave, C.tag, r_ids, r_wts, r_done);
+  // (the routing wave's activation stage, idle until its first task, holds the keys)
+  if (rwave < A.B) route_token(A, rwave, C.tag, r_ids, r_wts, r_done, (uint64_t*)C.act);
   // One task loop (one copy of the task code): the first routed task waits
   // for the workgroup's routing.
   Route rt{0ull, 0, r_ids, 0};
@@ -969,6 +976,10 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
   const int act_rows = B * 128 * 4;
   const int act_h = L.gf * kXPad * 4;
   L.lds_act = act_rows > act_h ? act_rows : act_h;
+  // a routing wave's stage first holds its 64 top-k keys and the selected weights
+  const int act_route = kWave * 8 + 8 * 4;
+  L.lds_act = L.lds_act > act_route ? L.lds_act : act_route;
+  L.lds_act = (L.lds_act + 15) & ~15;
   L.lds_bytes = (size_t)L.lds_x + 528 + (size_t)kWaves * L.lds_act;
   const int R = B * topk;
   const int slots = E < R ? E : R;
