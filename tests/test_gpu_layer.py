@@ -201,11 +201,13 @@ def test_prefill_matches_float64(oracle, full_int8, full_bf16, which, T) -> None
 
 
 @pytest.mark.parametrize(("int8", "group", "H", "F", "T"),
-                         [(True, 64, 384, 256, 40), (True, 256, 512, 256, 200), (False, 128, 384, 384, 130)],
-                         ids=["int8-G64-H384", "int8-G256-H512", "bf16-H384"])
+                         [(True, 64, 384, 256, 40), (True, 256, 512, 256, 200), (False, 128, 384, 384, 130),
+                          (True, 64, 1024, 1024, 70), (True, 64, 1280, 256, 90)],
+                         ids=["int8-G64-H384", "int8-G256-H512", "bf16-H384", "int8-G64-16groups", "int8-G64-20groups"])
 def test_prefill_small_shapes(oracle, int8, group, H, F, T) -> None:
     """Column tiles that overhang N (down N = 384 against 256-column tiles), scale groups of 64 and 256, short
-    and partial row tiles."""
+    and partial row tiles; 16 scale groups per weight row (the most a tile keeps in LDS) and 20 (gate/up on the
+    fragment-load kernel, down on the LDS-staged one)."""
     layer = oracle.make_layer(40 + H + group, E=8, H=H, F=F, n_shared=1, int8=int8, std=0.05, router_std=0.1,
                               group=group)
     moe = moe_for(layer)
@@ -252,6 +254,41 @@ def test_prefill_adversarial_routing(oracle, full_int8) -> None:
     got = n(out)
     ref = oracle.moe_layer_f64(x, adv, ids_o, wts_o, bf16_dequant=True)
     assert oracle.rel_err(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("which", ["int8", "bf16"])
+def test_prefill_every_tile_class(oracle, full_int8, full_bf16, which) -> None:
+    """Token groups steered onto chosen expert sets give experts 100, 127, 27, 50 and 70 rows: partial row
+    tiles of every active-block count for 128-row tiles (4, 4, 1, 2, 3) and 64-row tiles (2, 2, 1, 2, 1),
+    each computed once."""
+    import dataclasses
+
+    layer = full_int8 if which == "int8" else full_bf16
+    sizes = [100, 27, 50, 70]
+    sets = [np.arange(0, 6), np.arange(3, 9), np.arange(9, 15), np.arange(15, 21)]
+    T = sum(sizes)
+    x = oracle.rmsnorm_rows(np.random.default_rng(11), T, 1280)
+    router = layer.router.copy()
+    x[:, 1:5] = 0.0
+    router[:, 1:5] = 0.0
+    start = 0
+    for gi, (n_, st) in enumerate(zip(sizes, sets)):
+        x[start:start + n_, 1 + gi] = 10.0
+        router[st, 1 + gi] = 1.0
+        start += n_
+    steered = dataclasses.replace(layer, router=np.ascontiguousarray(router))
+    moe = moe_for(steered)
+    out, ids, wts = moe(t(x), routing=True)
+    ids_o, wts_o = oracle.moe_gate(x, steered.router, 6)
+    assert np.array_equal(n(ids), ids_o)
+    counts = np.bincount(ids_o.ravel(), minlength=64)
+    assert sorted(set(counts[:21].tolist())) == [27, 50, 70, 100, 127]
+    got = n(out)
+    ref = oracle.moe_layer_f64(x, steered, ids_o, wts_o, bf16_dequant=True)
+    rel = oracle.rel_err(got, ref)
+    print(f"[uocr] prefill {which} steered groups: rel {rel:.3e}")
+    assert rel <= 1e-2
+    assert min(oracle.cosine(got[i], ref[i]) for i in range(T)) > 0.999
 
 
 def test_prefill_rows_do_not_depend_on_the_batch(oracle, full_int8) -> None:

@@ -561,10 +561,11 @@ hipError_t launch_moe_gemm(const GemmProblem& routed, const GemmProblem& shared,
 // work, about ten VALU instructions per MFMA, bounds a lone wave).  A step is
 // 64 k: every weight row contributes 64 (int8) or 128 (bf16) contiguous bytes,
 // 4 or 8 lanes to a row, where the fragment-layout loads touch 32 rows per
-// instruction.  A stage holds the workgroup's 256 weight rows, the A step and
-// (int8) the step's scale of every weight row; kCount stages form a ring,
-// each loaded kCount - 1 steps ahead.  Each wave loads exactly the weight
-// rows and scales it reads, so only the shared A step needs the barrier.  The
+// instruction.  A stage holds the workgroup's 256 weight rows and the A step;
+// kCount stages form a ring, each loaded kCount - 1 steps ahead.  The int8
+// scales of the tile's weight rows (one contiguous block of rows x groups
+// floats per projection) are loaded into LDS once, at the tile's start: read
+// step by step they would touch a cache line per few rows every step.  The
 // waits are explicit (s_waitcnt vmcnt(n) before the barrier, n the loads
 // issued since the step's own): every thread issues the same number of loads
 // per step, the loads past the last step re-read it, and no other vector
@@ -579,25 +580,36 @@ template <WKind W>
 constexpr int kLdsBM = W == kInt8Rows ? 128 : 64;
 constexpr int kWgPerCu = 2;  // two workgroups share a CU: one's barrier waits overlap the other's work
 
+// LDS for an int8 tile's scales: 256 weight rows x up to 16 groups (K / 16
+// or coarser groups; finer ones go to the fragment-load kernel).
+constexpr int kMaxScaleGroups = 16;
+constexpr int kScaleLds = kWRowsWg * kMaxScaleGroups * 4;
+
 template <int BM, WKind W>
 struct Stage {
   static constexpr int kBRowBytes = W == kInt8Rows ? BK : 2 * BK;  // one step of a weight row
   static constexpr int kBBytes = kWRowsWg * kBRowBytes;
   static constexpr int kABytes = BM * 2 * BK;
-  static constexpr int kSBytes = W == kInt8Rows ? kWRowsWg * 4 : 0;
-  static constexpr int kBytes = kBBytes + kABytes + kSBytes;
-  static constexpr int kBudget = 160 * 1024 / kWgPerCu;
+  static constexpr int kBytes = kBBytes + kABytes;
+  static constexpr int kBudget = 160 * 1024 / kWgPerCu - (W == kInt8Rows ? kScaleLds : 0);
   static constexpr int kCount = kBudget / kBytes < 4 ? kBudget / kBytes : 4;
-  static constexpr int kBLoads = kBBytes / 1024 / 4;           // weight loads per thread per step
-  static constexpr int kALoads = kABytes / 16 / kGThreads;      // A loads per thread per step
-  static constexpr int kLoads = kBLoads + kALoads + (W == kInt8Rows ? 1 : 0);
+  static constexpr int kBLoads = kBBytes / 1024 / 4;  // weight loads per thread per step
+  // loads per thread per step of a tile with NACT active 32-row blocks: the
+  // weights and one 1 KB A load per block (32 rows x 128 bytes over 256 threads)
+  template <int NACT>
+  static constexpr int loads() {
+    return kBLoads + NACT;
+  }
   static_assert(kCount >= 2, "two stages");
+  static_assert(kABytes == (BM / 32) * 16 * kGThreads, "one A load per thread per 32-row block");
 };
 
 template <WKind W>
 constexpr int kRing = Stage<kLdsBM<W>, W>::kBytes * Stage<kLdsBM<W>, W>::kCount;
+template <WKind W>
+constexpr int kTileLds = kRing<W> + (W == kInt8Rows ? kScaleLds : 0);  // the scales follow the ring
 template <WKind W0>
-constexpr int kLdsBytes = kRing<W0> > kRing<kBf16KBlocked> ? kRing<W0> : kRing<kBf16KBlocked>;
+constexpr int kLdsBytes = kTileLds<W0> > kTileLds<kBf16KBlocked> ? kTileLds<W0> : kTileLds<kBf16KBlocked>;
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 __device__ __forceinline__ void dma16(const void* g, void* l) {
@@ -621,14 +633,15 @@ __device__ __forceinline__ void step_barrier() {
 // put a chunk in different banks.
 __device__ __forceinline__ int swz64(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 
-// One step from a stage: 4 MFMA sub-steps, lane half h at k = 32h + 8 sub.
-// The wave's weight bytes of the step are read first, and the A fragments of
-// sub-step k + 1 before the MFMAs of sub-step k.
-template <int BM, WKind W>
-__device__ __forceinline__ void lds_step(f32x16 (&acc)[BM / 32][2], const char* st, int w, int m, int h,
-                                         int nact) {
+// One step from a stage: 4 MFMA sub-steps, lane half h at k = 32h + 8 sub,
+// over the tile's NACT active 32-row blocks (the rows past them are not
+// computed).  The wave's weight bytes of the step are read first, and the A
+// fragments of sub-step k + 1 before the MFMAs of sub-step k.
+template <int BM, WKind W, int NACT>
+__device__ __forceinline__ void lds_step(f32x16 (&acc)[NACT][2], const char* st, const float (&sc)[2], int w, int m,
+                                         int h) {
   using St = Stage<BM, W>;
-  constexpr int MB = BM / 32;
+  constexpr int MB = NACT;
   constexpr int RB = St::kBRowBytes;
   constexpr int NQ = W == kInt8Rows ? 2 : 4;  // the lane's 16-byte weight chunks per block
   const char* Bw = st + 64 * w * RB;          // the wave's 64 weight rows
@@ -649,22 +662,14 @@ __device__ __forceinline__ void lds_step(f32x16 (&acc)[BM / 32][2], const char* 
         raw[b][q] = *(const i32x4*)(Bw + (32 * b + m) * RB + 16 * (c ^ (W == kInt8Rows ? swz64(m) : sw)));
       }
     }
-  float sc[2] = {1.0f, 1.0f};
-  if constexpr (W == kInt8Rows) {
-    const float* S = (const float*)(st + St::kBBytes + St::kABytes);
-#pragma unroll
-    for (int b = 0; b < 2; ++b) sc[b] = S[64 * w + 32 * b + m];
-  }
-  // 32-row blocks past the tile's rows (nact of them hold rows) are skipped.
-  // 64-row tiles read the A fragments of sub-step k + 1 during sub-step k;
-  // 128-row tiles read each sub-step's own (registers for two waves a SIMD),
-  // the other workgroup on the CU covering the wait.
+  // Up to two blocks read the A fragments of sub-step k + 1 during sub-step
+  // k; more read each sub-step's own (registers for two waves a SIMD), the
+  // other workgroup on the CU covering the wait.
   constexpr int AB = MB > 2 ? 1 : 2;
   bf16x8 a[AB][MB];
   auto read_a = [&](bf16x8(&dst)[MB], int sub) {
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
-      if (i < nact) dst[i] = *(const bf16x8*)(A + (32 * i + m) * 2 * BK + 16 * ((4 * h + sub) ^ sw));
+    for (int i = 0; i < MB; ++i) dst[i] = *(const bf16x8*)(A + (32 * i + m) * 2 * BK + 16 * ((4 * h + sub) ^ sw));
   };
   if constexpr (AB == 2) read_a(a[0], 0);
 #pragma unroll
@@ -691,10 +696,8 @@ __device__ __forceinline__ void lds_step(f32x16 (&acc)[BM / 32][2], const char* 
     }
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
-      if (i < nact) {
-        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[0], acc[i][0], 0, 0, 0);
-        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[1], acc[i][1], 0, 0, 0);
-      }
+      acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[0], acc[i][0], 0, 0, 0);
+      acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[1], acc[i][1], 0, 0, 0);
     }
     // keep each sub-step's dequantisation next to its MFMAs (the two issue in
     // turn on a SIMD anyway): hoisting it only lengthens register lifetimes
@@ -702,10 +705,13 @@ __device__ __forceinline__ void lds_step(f32x16 (&acc)[BM / 32][2], const char* 
   }
 }
 
-template <int BM, WKind W, int NPROJ>
-__device__ void lds_tile(const GemmProblem& P, const TileRef& t, char* lds) {
+// One tile whose rows fill NACT 32-row blocks: only those blocks' A rows are
+// loaded and computed.
+template <int BM, WKind W, int NPROJ, int NACT>
+__device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t, char* lds) {
   using St = Stage<BM, W>;
-  constexpr int NS = St::kCount, NB = St::kBLoads, NA = St::kALoads;
+  constexpr int NS = St::kCount, NB = St::kBLoads, NA = NACT;
+  constexpr int NL = St::template loads<NACT>();
   constexpr int RB = St::kBRowBytes;
   constexpr int RPL = 1024 / RB;  // weight rows per load
   const int tid = (int)threadIdx.x;
@@ -744,26 +750,39 @@ __device__ void lds_tile(const GemmProblem& P, const TileRef& t, char* lds) {
   }
   const int64_t bstep = W == kBf16KBlocked ? (int64_t)(BK / 16) * P.N * 32 : RB;
 
-  // A: load i of the step fills chunk j % 8 of stage row (64 (w NA + i) + j) / 8
+  // A: load i of the step fills 1 KB unit 4i + w of the A stage, chunk j % 8 of
+  // stage row 8 (4i + w) + j / 8
   int aoff[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int r = ((w * NA + i) * 64 + j) >> 3;
+    const int r = 8 * (4 * i + w) + (j >> 3);
     const int c = (j & 7) ^ swz(r);
     const int pos = t.pos0 + min(r, t.rows - 1);
     const int row = (P.a_by_token && P.rows.n_groups != nullptr) ? ldg(P.rows.group_rows + pos) / P.x_div : pos;
     aoff[i] = (int)((int64_t)row * P.lda) + 8 * c;
   }
 
-  // int8 scales: lane j of wave w loads the scale of stage row 64w + j
-  const float* ssrc = nullptr;
-  float ginv = 0.0f;
+  // int8 scales, loaded once for the tile after the ring: NPROJ 1, [256 rows
+  // from n0][G]; NPROJ 2, [128 gate rows from n0][G] then the up rows'.  Each
+  // projection's block is contiguous in [E][N][G]; rows past N re-read the
+  // last real scale.  64-float units, G of them per wave; these loads precede
+  // the stages', so the first step's wait covers them.
+  float* sl = (float*)(lds + kRing<W>);
+  int srow[2] = {0, 0};  // this lane's rows of blocks 0 and 1, times G
   if constexpr (W == kInt8Rows) {
-    const int b = j >> 5;
-    const int row = min(NPROJ == 2 ? t.n0 + 32 * w + m : t.n0 + 64 * w + j, P.N - 1);
-    ssrc = (NPROJ == 2 && b == 1 ? P.p[1].s : P.p[0].s) + ((int64_t)t.e * P.N + row) * P.groups;
-    ginv = (float)P.groups / (float)P.K;  // 1 / group width
+    const int G = P.groups;
+    constexpr int PR = NPROJ == 2 ? 128 : 256;  // rows per projection block
+    const int64_t base = ((int64_t)t.e * P.N + t.n0) * G;
+    const int lim = min(PR, P.N - t.n0) * G - 1;
+    for (int u = w; u < 4 * G; u += 4) {
+      const bool up = NPROJ == 2 && u >= 2 * G;
+      const int f = 64 * (up ? u - 2 * G : u) + j;
+      dma4((up ? P.p[1].s : P.p[0].s) + base + min(f, lim), sl + 64 * u);
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) srow[b] = (NPROJ == 2 ? PR * b + 32 * w + m : 64 * w + 32 * b + m) * G;
   }
+  const int spg = W == kInt8Rows ? P.K / P.groups / BK : 1;  // steps per scale group
 
   // the loads of step s (clamped to the last step) into stage s % NS
   auto issue = [&](int s) {
@@ -777,45 +796,84 @@ __device__ void lds_tile(const GemmProblem& P, const TileRef& t, char* lds) {
         dma16(bsrc[i] + sc * bstep, st + (64 * w + RPL * i) * RB);
     }
 #pragma unroll
-    for (int i = 0; i < NA; ++i) dma16(P.a + aoff[i] + sc * BK, st + St::kBBytes + (w * NA + i) * 1024);
-    if constexpr (W == kInt8Rows) {
-      // the group of the step's k (k < 2^16: the float quotient of k + 1/2 truncates to it exactly)
-      const int g = (int)(((float)(sc * BK) + 0.5f) * ginv);
-      dma4(ssrc + g, st + St::kBBytes + St::kABytes + 64 * w * 4);
-    }
+    for (int i = 0; i < NA; ++i) dma16(P.a + aoff[i] + sc * BK, st + St::kBBytes + (4 * i + w) * 1024);
   };
 
-  f32x16 acc[BM / 32][2];
+  f32x16 acc[NACT][2];
 #pragma unroll
-  for (int i = 0; i < BM / 32; ++i)
+  for (int i = 0; i < NACT; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][0][r] = acc[i][1][r] = 0.0f;
+  int g = 0, gs = 0;  // the step's scale group, and steps into it
+  auto compute = [&](int s) {
+    float sc[2] = {1.0f, 1.0f};
+    if constexpr (W == kInt8Rows) {
+      sc[0] = sl[srow[0] + g];
+      sc[1] = sl[srow[1] + g];
+      const bool next = ++gs == spg;
+      g += next;
+      gs = next ? 0 : gs;
+    }
+    lds_step<BM, W, NACT>(acc, lds + (s % NS) * St::kBytes, sc, w, m, h);
+  };
+  // S is even and at least 2, so the NS - 1 <= 2 prologue steps exist; the
+  // last NS - 1 steps load nothing, and no load is in flight when the tile ends
+  static_assert(NS >= 2 && NS <= 3, "ring depth");
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i) issue(i);
-  const int nact = __builtin_amdgcn_readfirstlane((t.rows + 31) >> 5);
-  for (int s = 0; s < S; ++s) {
-    step_barrier<(NS - 2) * St::kLoads>();
+  for (int s = 0; s < S - (NS - 1); ++s) {
+    step_barrier<(NS - 2) * NL>();
     issue(s + NS - 1);  // into the stage read in step s - 1, which every wave has finished
-    lds_step<BM, W>(acc, lds + (s % NS) * St::kBytes, w, m, h, nact);
+    compute(s);
   }
-  // every wave has finished reading the stages before the next tile's loads
-  step_barrier<(NS - 1) * St::kLoads>();
-  store_tile<BM, NPROJ>(P, t, acc, w, m, h);
+#pragma unroll
+  for (int u = 0; u < NS - 1; ++u) {
+    // tail step S - (NS - 1) + u: its loads and the NS - 2 - u stages after it are the ones outstanding
+    if constexpr (NS == 3) {
+      if (u == 0)
+        step_barrier<NL>();
+      else
+        step_barrier<0>();
+    } else {
+      step_barrier<0>();
+    }
+    compute(S - (NS - 1) + u);
+  }
+  // every wave has finished reading the stages (and the scales) before the next tile's loads
+  step_barrier<0>();
+  store_tile<32 * NACT, NPROJ>(P, t, acc, w, m, h);
 }
 
-// Balanced placement for the LDS-staged path.  The tiles of a range (row
-// tile major) are cut into pieces of about total / (8 kPiecesPerXcd) tiles,
-// whole row tiles each, and the pieces are dealt round robin to the XCDs in
-// range order, so each XCD's share is within one piece of the mean while a
-// piece's row tiles still share their weight tiles in one L2.  Every wave
-// plans for its XCD with a 128-int scratch of its own in LDS.
-constexpr int kPiecesPerXcd = 8;
+// Placement for the LDS-staged path.  A unit is one column tile of one
+// group and a run of its row tiles (a routed expert's unit has all of them,
+// so each expert weight tile is fetched into one L2 and serves all of its
+// rows there; the shared experts' many row tiles are cut into at most 8
+// runs).  Units are dealt round robin to the XCDs (routed first, the shared
+// ones numbered on): an expert's 5-8 column tiles land on as many XCDs, so a
+// hot expert is spread over the chip.
+//
+// Order.  A tile's cost grows with its active 32-row blocks, and an int8
+// tile's much more than a bf16 one's (the dequantisation is paid per tile).
+// An XCD's tiles are listed class by class in decreasing estimated cost
+// (class: problem and active blocks; within a class, unit order), and its
+// workgroup j walks tiles j, j + J, ... of the list: the costly tiles start
+// first and the last round is made of short ones.  (A work queue -- atomic
+// per-XCD counters, tiles taken as workgroups finish them -- measured slower
+// on this GPU: the counter round trips and their broadcast cost more than
+// the balance gained.)
 
-struct Pieces {
-  int prefix;  // lane v: inclusive prefix of the tile counts of the XCD's pieces 0..v
-  int rk;      // lane v: range << 16 | index of the piece within its range
-  int q;       // tiles per piece (target)
-  int total;   // pieces of the problem
+constexpr int kMaxUnits = 1024;  // per problem: 128 per XCD, two a lane
+
+struct Units {  // lane v holds the XCD's units v and v + 64 of its problem (hh = 0, 1)
+  int nfull[2];  // tiles in full row tiles (BM rows)
+  int npart[2];  // 1 if the unit has the group's last row tile and that one is partial
+  int apart[2];  // the active 32-row blocks of that row tile
+  int mt0[2];    // first row tile of the unit
+  int c[2];      // column tile
+  int start[2];  // the group's first row position
+  int count[2];  // the group's rows
+  int e[2];      // the group's expert (routed)
+  int n;         // units of the problem (all XCDs)
 };
 
 __device__ __forceinline__ int wave_sum_i(int v) {
@@ -833,94 +891,133 @@ __device__ __forceinline__ int wave_scan_i(int v) {  // inclusive
   return v;
 }
 
-// Pieces of problem P for XCD x, dealt from XCD u0 on (piece u of the problem
-// to XCD (u0 + u) % 8); at most 128 ranges and 512 pieces.
+// Problem P's units on XCD x, unit u going to XCD (u0 + u) % 8 (at most 1024
+// units).  Routed: unit u = group u / nt, column u % nt, every row tile.
+// Dense: run u / nt of ceil(row tiles / 8) row tiles, column u % nt.
 template <int BM>
-__device__ Pieces plan_pieces(const GemmProblem& P, const Plan& p, int x, int u0, int* sc) {
-  const int l = lane_id();
-  const int R = p.ng * p.nr;
-  int items[2], tiles[2], cols[2];
+__device__ __forceinline__ Units plan_units(const GemmProblem& P, int nt, int ng, int x, int u0) {
+  const bool routed = P.rows.n_groups != nullptr;
+  const int rt_dense = (P.M + BM - 1) / BM;
+  const int run = routed ? 1 << 30 : max(1, (rt_dense + kXcds - 1) / kXcds);
+  const int nrun = routed ? 1 : (rt_dense + run - 1) / run;
+  Units q;
+  q.n = routed ? ng * nt : (P.M > 0 ? nrun * nt : 0);
+  const int xs = ((x - u0) % kXcds + kXcds) % kXcds;
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    const int r = l + 64 * hh;
-    items[hh] = tiles[hh] = 0;
-    cols[hh] = 1;
-    if (r < R) {
-      const int g = r / p.nr;
-      const int c = r - g * p.nr;
-      cols[hh] = min(p.per, p.nt - c * p.per);
-      tiles[hh] = row_tiles<BM>(P, g);
-      items[hh] = tiles[hh] * cols[hh];
+    const int u = xs + kXcds * (lane_id() + 64 * hh);
+    q.nfull[hh] = q.npart[hh] = q.apart[hh] = q.mt0[hh] = q.c[hh] = q.start[hh] = q.count[hh] = q.e[hh] = 0;
+    if (u < q.n) {
+      const int g = routed ? u / nt : 0;
+      const int ri = routed ? 0 : u / nt;  // row run (dense)
+      int start = 0, count = P.M, e = 0;
+      if (routed) {
+        start = ldg(P.rows.group_start + g);
+        count = ldg(P.rows.group_start + g + 1) - start;
+        e = ldg(P.rows.group_expert + g);
+      }
+      const int rt = (count + BM - 1) / BM;
+      const int mt0 = routed ? 0 : ri * run;
+      const int mt1 = min(rt, mt0 + run);
+      const int rem = count - (rt - 1) * BM;  // rows of the group's last row tile
+      const bool part = count > 0 && rem < BM && mt1 == rt;
+      q.nfull[hh] = mt1 - mt0 - (part ? 1 : 0);
+      q.npart[hh] = part ? 1 : 0;
+      q.apart[hh] = part ? (rem + 31) >> 5 : 0;
+      q.mt0[hh] = mt0;
+      q.c[hh] = u % nt;
+      q.start[hh] = start;
+      q.count[hh] = count;
+      q.e[hh] = e;
     }
   }
-  const int total = wave_sum_i(items[0] + items[1]);
-  const int q = max(1, (total + kXcds * kPiecesPerXcd - 1) / (kXcds * kPiecesPerXcd));
-  int np[2];
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
-    const int pr = max(1, (q + cols[hh] - 1) / cols[hh]);  // row tiles per piece
-    np[hh] = (tiles[hh] + pr - 1) / pr;
-  }
-  const int inc0 = wave_scan_i(np[0]);
-  const int tot0 = __builtin_amdgcn_readlane(inc0, kWave - 1);
-  const int inc1 = wave_scan_i(np[1]) + tot0;
-  const int totp = __builtin_amdgcn_readlane(inc1, kWave - 1);
-  sc[l] = inc0 - np[0];  // first piece of range l
-  sc[64 + l] = inc1 - np[1];
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's own stores, before it reads them
-  // this lane's piece: the v-th of XCD x
-  const int xs = (x - u0 % kXcds + kXcds) % kXcds;
-  const int u = xs + kXcds * l;
-  int it = 0, rk = 0;
-  if (u < totp) {
-    int lo = 0, hi = R - 1;  // the last range whose first piece is <= u (every range has a piece)
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (sc[mid] <= u)
-        lo = mid;
-      else
-        hi = mid - 1;
-    }
-    const int r = lo;
-    const int k = u - sc[r];
-    const int g = r / p.nr;
-    const int c = r - g * p.nr;
-    const int cl = min(p.per, p.nt - c * p.per);
-    const int pr = max(1, (q + cl - 1) / cl);
-    const int rows = min(pr, row_tiles<BM>(P, g) - k * pr);
-    it = rows * cl;
-    rk = (r << 16) | k;
-  }
-  return Pieces{wave_scan_i(it), rk, q, totp};
+  return q;
 }
 
-// Tile `it` of the XCD's pieces.
+// A unit's tiles with nact active blocks: its full row tiles (nact = BM / 32),
+// then its partial row tile if that has nact blocks.
 template <int BM>
-__device__ TileRef piece_tile(const GemmProblem& P, const Plan& p, const Pieces& pc, int it, int bn) {
-  const int v = (int)__popcll(__ballot(pc.prefix <= it));
-  const int before = v > 0 ? __builtin_amdgcn_readlane(pc.prefix, v - 1) : 0;
-  const int rk = __builtin_amdgcn_readlane(pc.rk, v);
-  const int r = rk >> 16, k = rk & 0xffff;
-  const int g = r / p.nr;
-  const int c = r - g * p.nr;
-  const int cols = min(p.per, p.nt - c * p.per);
-  const int pr = max(1, (pc.q + cols - 1) / cols);
+__device__ __forceinline__ int class_count(const Units& q, int hh, int nact) {
+  return (nact == BM / 32 ? q.nfull[hh] : 0) + (q.apart[hh] == nact ? q.npart[hh] : 0);
+}
+
+// Tile `it` of class (nact active blocks) in the XCD's units (lanes' hh = 0
+// units, then hh = 1).
+template <int BM>
+__device__ __forceinline__ TileRef class_tile(const GemmProblem& P, const Units& q, int nact, int it, int bn) {
+  const int inc0 = wave_scan_i(class_count<BM>(q, 0, nact));
+  const int tot0 = __builtin_amdgcn_readlane(inc0, kWave - 1);
+  const int hh = it >= tot0 ? 1 : 0;
+  const int inc = hh ? wave_scan_i(class_count<BM>(q, 1, nact)) + tot0 : inc0;
+  const int lane = (int)__popcll(__ballot(inc <= it));
+  const int before = lane > 0 ? __builtin_amdgcn_readlane(inc, lane - 1) : (hh ? tot0 : 0);
   const int local = it - before;
-  const int mt = k * pr + local / cols;
+  const int nfull = nact == BM / 32 ? __builtin_amdgcn_readlane(hh ? q.nfull[1] : q.nfull[0], lane) : 0;
+  const int count = __builtin_amdgcn_readlane(hh ? q.count[1] : q.count[0], lane);
+  const int mt = local < nfull ? __builtin_amdgcn_readlane(hh ? q.mt0[1] : q.mt0[0], lane) + local : (count - 1) / BM;
   TileRef t;
-  t.n0 = (c * p.per + local % cols) * bn;
-  if (P.rows.n_groups == nullptr) {
-    t.e = 0;
-    t.pos0 = mt * BM;
-    t.rows = min(BM, P.M - t.pos0);
-  } else {
-    const int start = ldg(P.rows.group_start + g);
-    const int count = ldg(P.rows.group_start + g + 1) - start;
-    t.e = ldg(P.rows.group_expert + g);
-    t.pos0 = start + mt * BM;
-    t.rows = min(BM, count - mt * BM);
-  }
+  t.n0 = __builtin_amdgcn_readlane(hh ? q.c[1] : q.c[0], lane) * bn;
+  t.pos0 = __builtin_amdgcn_readlane(hh ? q.start[1] : q.start[0], lane) + mt * BM;
+  t.rows = min(BM, count - mt * BM);
+  t.e = __builtin_amdgcn_readlane(hh ? q.e[1] : q.e[0], lane);
   return t;
+}
+
+// The classes of a launch in decreasing estimated cost, and an XCD's tiles
+// of each.  Class k: problem cls[k] >> 8 (0 routed, 1 shared), cls[k] & 255
+// active blocks.  Estimated cost per 64-k step: 100 + 35 per block for int8
+// weights, 45 + 25 per block for bf16 (measured tile times fit these within
+// about 15 %).
+constexpr int kMaxClasses = 6;
+struct Sched {
+  int n;
+  int cls[kMaxClasses];
+  int cnt[kMaxClasses];
+  int total;
+};
+
+__device__ __forceinline__ int tile_cost(const GemmProblem& P, int nact) {
+  return (P.K / BK) * (P.kind == kInt8Rows ? 100 + 35 * nact : 45 + 25 * nact);
+}
+
+template <int BMA, int BMB>
+__device__ __forceinline__ Sched make_sched(const GemmProblem& a, const GemmProblem& b, const Units& qa,
+                                            const Units& qb) {
+  constexpr int MA = BMA / 32, MB = BMB / 32;
+  static_assert(MA + MB <= kMaxClasses, "classes");
+  Sched sd;
+  int key[kMaxClasses];
+  sd.n = MA + MB;
+#pragma unroll
+  for (int k = 0; k < kMaxClasses; ++k) {
+    const bool isa = k < MA;
+    const int nact = isa ? MA - k : MA + MB - k;
+    sd.cls[k] = k < MA + MB ? ((isa ? 0 : 1) << 8) | nact : 0;
+    key[k] = k < MA + MB ? tile_cost(isa ? a : b, nact) : -1;
+  }
+  // stable sort by decreasing cost (a fixed exchange network on uniform values)
+#pragma unroll
+  for (int i = 0; i < kMaxClasses; ++i)
+#pragma unroll
+    for (int k = kMaxClasses - 1; k > i; --k)
+      if (key[k] > key[k - 1]) {
+        const int tk = key[k], tc = sd.cls[k];
+        key[k] = key[k - 1];
+        sd.cls[k] = sd.cls[k - 1];
+        key[k - 1] = tk;
+        sd.cls[k - 1] = tc;
+      }
+  sd.total = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxClasses; ++k) {
+    const int prob = sd.cls[k] >> 8, nact = sd.cls[k] & 255;
+    const int v = k >= sd.n ? 0
+                  : prob ? class_count<BMB>(qb, 0, nact) + class_count<BMB>(qb, 1, nact)
+                         : class_count<BMA>(qa, 0, nact) + class_count<BMA>(qa, 1, nact);
+    sd.cnt[k] = __builtin_amdgcn_readfirstlane(wave_sum_i(v));
+    sd.total += sd.cnt[k];
+  }
+  return sd;
 }
 
 template <WKind W0, int NP>
@@ -929,23 +1026,55 @@ __global__ void __launch_bounds__(kGThreads, kWgPerCu) k_moe_gemm_lds(GemmProble
   constexpr int bn = kWRowsWg / NP;
   constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
   const int x = (int)blockIdx.x % kXcds;
+  const int nta = (a.N + bn - 1) / bn, ntb = (b.N + bn - 1) / bn;
+  const int nga = a.rows.n_groups != nullptr ? ldc(a.rows.n_groups) : 1;
   const int j = (int)blockIdx.x / kXcds;
   const int J = (int)gridDim.x / kXcds;
-  const Plan pa = plan_of(a, bn);
-  const Plan pb = plan_of(b, bn);
-  // each wave plans in its own 512 bytes of the (not yet used) stage ring
-  int* sc = (int*)lds_stages + (threadIdx.x >> 6) * 128;
-  const Pieces qa = plan_pieces<BMA>(a, pa, x, 0, sc);
-  const Pieces qb = plan_pieces<BMB>(b, pb, x, qa.total, sc);  // dealt on from where a's ended
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave done with its scratch
-  const int na = __builtin_amdgcn_readlane(qa.prefix, kWave - 1);
-  const int nb = __builtin_amdgcn_readlane(qb.prefix, kWave - 1);
-  for (int it = j; it < na + nb; it += J) {
-    if (it < na)
-      lds_tile<BMA, W0, NP>(a, piece_tile<BMA>(a, pa, qa, it, bn), lds_stages);
-    else
-      lds_tile<BMB, kBf16KBlocked, NP>(b, piece_tile<BMB>(b, pb, qb, it - na, bn), lds_stages);
-  }
+  const Units qa = plan_units<BMA>(a, nta, nga, x, 0);
+  const Units qb = plan_units<BMB>(b, ntb, 1, x, qa.n);  // dealt on from where the routed units ended
+  const Sched sd = make_sched<BMA, BMB>(a, b, qa, qb);
+  // tile `it` of the XCD's list: its class, then the class's tile
+  auto run = [&](int it) __attribute__((always_inline)) {
+    int cls = sd.cls[0];
+    bool found = false;
+#pragma unroll
+    for (int k = 0; k < kMaxClasses; ++k) {
+      if (!found && k < sd.n) {
+        if (it < sd.cnt[k]) {
+          cls = sd.cls[k];
+          found = true;
+        } else {
+          it -= sd.cnt[k];
+        }
+      }
+    }
+    const int nact = cls & 255;
+    if ((cls >> 8) == 0) {
+      if constexpr (BMA == 128) {
+        if (nact == 4)
+          lds_tile<BMA, W0, NP, 4>(a, class_tile<BMA>(a, qa, 4, it, bn), lds_stages);
+        else if (nact == 3)
+          lds_tile<BMA, W0, NP, 3>(a, class_tile<BMA>(a, qa, 3, it, bn), lds_stages);
+        else if (nact == 2)
+          lds_tile<BMA, W0, NP, 2>(a, class_tile<BMA>(a, qa, 2, it, bn), lds_stages);
+        else
+          lds_tile<BMA, W0, NP, 1>(a, class_tile<BMA>(a, qa, 1, it, bn), lds_stages);
+      } else {
+        static_assert(BMA == 64, "64- or 128-row tiles");
+        if (nact == 2)
+          lds_tile<BMA, W0, NP, 2>(a, class_tile<BMA>(a, qa, 2, it, bn), lds_stages);
+        else
+          lds_tile<BMA, W0, NP, 1>(a, class_tile<BMA>(a, qa, 1, it, bn), lds_stages);
+      }
+    } else {
+      static_assert(BMB == 64, "64-row shared tiles");
+      if (nact == 2)
+        lds_tile<BMB, kBf16KBlocked, NP, 2>(b, class_tile<BMB>(b, qb, 2, it, bn), lds_stages);
+      else
+        lds_tile<BMB, kBf16KBlocked, NP, 1>(b, class_tile<BMB>(b, qb, 1, it, bn), lds_stages);
+    }
+  };
+  for (int it = j; it < sd.total; it += J) run(it);
 }
 
 template <WKind W0, int NP>
@@ -1000,6 +1129,19 @@ hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared
   if (routed.N % 32 || shared.N % 32 || routed.K % (2 * BK) || shared.K % (2 * BK)) return hipErrorInvalidValue;
   if (routed.kind == kInt8Rows && (routed.K % routed.groups || (routed.K / routed.groups) % BK))
     return hipErrorInvalidValue;
+  const int bn = kWRowsWg / (gu ? 2 : 1);
+  const int64_t units = (int64_t)routed.max_groups * ((routed.N + bn - 1) / bn);
+  const int64_t shared_units = (int64_t)kXcds * ((shared.N + bn - 1) / bn);
+  if ((routed.kind == kInt8Rows && routed.groups > kMaxScaleGroups) || units > kMaxUnits ||
+      shared_units > kMaxUnits) {
+    // groups finer than K / 16 (the fragment-load kernel reads each step's scale itself), or more
+    // routed units than the LDS-staged kernel's plan holds
+    if (routed.kind == kInt8Rows)
+      return gu ? launch_moe_gemm<64, kInt8Rows, 2, false>(routed, shared, s, name)
+                : launch_moe_gemm<64, kInt8Rows, 1, false>(routed, shared, s, name);
+    return gu ? launch_moe_gemm<64, kBf16Rows, 2, false>(routed, shared, s, name)
+              : launch_moe_gemm<64, kBf16Rows, 1, false>(routed, shared, s, name);
+  }
   if (!vec) {  // weights at any alignment: 64-row tiles only
     if (bm != 64) return hipErrorInvalidValue;
     if (routed.kind == kInt8Rows)
