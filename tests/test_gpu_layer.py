@@ -116,7 +116,7 @@ def test_decode_small_layer_bitwise(oracle, small, int8, decode_path) -> None:
     assert bits_equal(n(out), want)
 
 
-@pytest.mark.parametrize("B", [1, 3, 8])
+@pytest.mark.parametrize("B", [1, 2, 3, 8])  # 1 and 2 take the shared-first task order
 def test_decode_full_int8_bitwise(oracle, full_int8, B, decode_path) -> None:
     moe = moe_for(full_int8)
     x = oracle.rmsnorm_rows(np.random.default_rng(100 + B), B, 1280)
@@ -134,7 +134,7 @@ def test_decode_full_int8_bitwise(oracle, full_int8, B, decode_path) -> None:
         assert bits_equal(got, single)
 
 
-@pytest.mark.parametrize("B", [1, 8])
+@pytest.mark.parametrize("B", [1, 2, 8])
 def test_decode_full_bf16_bitwise(oracle, full_bf16, B, decode_path) -> None:
     moe = moe_for(full_bf16)
     x = oracle.rmsnorm_rows(np.random.default_rng(200 + B), B, 1280)
