@@ -45,10 +45,13 @@
 // waited for, so the launch still ends with NaN in the outputs that depend on
 // it; while the word stays set, every later launch on the slot writes NaN,
 // until the host reads and clears it (uocr_moe_fused_errors).  The
-// launch tag is the control word EPOCH + 1: every wave reads EPOCH at its
-// start, each workgroup then adds one to ARRIVED (a non-returning atomic),
-// and the last of the comb tasks (the only counter, H/64 x B increments) waits
-// for ARRIVED to reach the grid, clears both counters and advances EPOCH.
+// launch tag is the control word EPOCH + 1: every workgroup reads EPOCH at its
+// start and then adds one to its ARRIVED counter; the workgroup whose
+// addition completes the grid's count (known once its control wave has
+// finished its tasks, so the atomics' round trips stay off the other waves'
+// work) clears the counters and advances EPOCH.  Every workgroup has read
+// EPOCH by then, and the next launch on the stream starts after this one
+// ends, so no wave ever takes another launch's tag.
 // The tagged buffers and control words are library-owned and zeroed when
 // allocated; tags start at 1, so no zeroed word is ever taken for data.
 #include "uocr_device.h"
@@ -71,14 +74,12 @@ constexpr int kXPad = kFusedXPad;
 //   C_EPOCH   + k * kLine, k < kSpread: the epoch, one copy per line;
 //             workgroup b reads copy b % kSpread at its start
 //   C_ARRIVED + k * kLine, k < kSpread: workgroups arrived, workgroup b adds
-//             to counter b % kSpread
-//   C_COMBINED + k * kLine, k < kCombGroups: comb tasks done, comb task c
-//             adds to counter c % kCombGroups; the last of a group adds to
-//             C_COMBINED2, and the last of those is the launch's last comb
-constexpr int kLine = 32, kSpread = 32, kCombGroups = 8;
-constexpr int C_ERR = 4, C_COMBINED2 = kLine, C_EPOCH = 2 * kLine, C_ARRIVED = C_EPOCH + kSpread * kLine,
-              C_COMBINED = C_ARRIVED + kSpread * kLine;
-static_assert(C_COMBINED + kCombGroups * kLine <= kFusedCtlWords, "control words");
+//             to counter b % kSpread; the workgroup that completes a
+//             counter adds to C_ARRIVED2, and the one that completes that
+//             is the launch's last
+constexpr int kLine = 32, kSpread = 32;
+constexpr int C_ERR = 4, C_ARRIVED2 = kLine, C_EPOCH = 2 * kLine, C_ARRIVED = C_EPOCH + kSpread * kLine;
+static_assert(C_ARRIVED + kSpread * kLine <= kFusedCtlWords, "control words");
 
 // Workgroup b runs on XCD b % kXcds (the dispatcher deals workgroups to the
 // XCDs round robin).  Every XCD computes all the logits itself into its own
@@ -741,10 +742,8 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
 }
 
 // 64 columns of token t's output: sh = shared-down chunk partials added in
-// order; out = fma chain over j of w_j * y_j from 0, plus sh.  The last comb
-// task of the launch advances the launch tag.
-__device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, const Ctx& C, const Task& k,
-                                                         uint32_t epoch) {
+// order; out = fma chain over j of w_j * y_j from 0, plus sh.
+__device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   constexpr int kMaxG = 16;
   constexpr int kMaxK = 8;
   const int l = lane();
@@ -766,41 +765,11 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   for (int j = 0; j < kMaxK; ++j)
     if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
   A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : acc + shv;
-  // two-level count of the comb tasks: c is this task's ordinal among them
-  const int c = k.a * A.B + t;
-  const int grp = c % kCombGroups;
-  const int in_grp = (A.n_comb - grp + kCombGroups - 1) / kCombGroups;
-  const int groups = min(A.n_comb, kCombGroups);
-  uint32_t old = 0;
-  if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED + grp * kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = shfl(old, 0);
-  if (old + 1u != (uint32_t)in_grp) return;
-  if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_COMBINED2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = shfl(old, 0);
-  if (old + 1u != (uint32_t)groups) return;
-  // the launch's last comb task: once every workgroup has read the epoch, reset
-  // the counters and advance it
-  uint32_t spin = A.spin_limit;
-  for (;;) {
-    const uint32_t arrived = l < kSpread ? ld_word(A.ctl + C_ARRIVED + l * kLine) : 0u;
-    if (poll_done(tree_sum_u32(arrived) >= gridDim.x, spin, A.ctl)) break;
-  }
-  // A workgroup that never arrived may still start: the counters and the
-  // epoch then stay as they are (that late workgroup takes this launch's tag),
-  // and the error word keeps later launches' outputs NaN until the host clears
-  // the slot.
-  if (expired(spin)) return;
-  if (l < kSpread) {
-    st_word(A.ctl + C_ARRIVED + l * kLine, 0u);
-    if (l < kCombGroups) st_word(A.ctl + C_COMBINED + l * kLine, 0u);
-    if (l == 0) st_word(A.ctl + C_COMBINED2, 0u);
-    st_word(A.ctl + C_EPOCH + l * kLine, epoch + 1u);
-  }
 }
 
 // Runs task t.
 __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, const Ctx& C0, const Route& rt, int t,
-                                                        const Task& k, uint32_t epoch, int64_t troute) {
+                                                        const Task& k, int64_t troute) {
   Ctx C = C0;
   C.t = t;
   UOCR_TRACE(A, t, 0);
@@ -821,7 +790,7 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
       else
         task_rdn<false>(A, C, rt, k);
       break;
-    case K_COMB: task_comb(A, C, k, epoch); break;
+    case K_COMB: task_comb(A, C, k); break;
     default: break;
   }
   UOCR_TRACE(A, t, 2);
@@ -910,9 +879,11 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   __syncthreads();
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(*lds_epoch);
   C.tag = epoch + 1u;
+  // the arrival count; its returned value is read after the control wave's tasks
+  uint32_t arrived = 0u;
   if (threadIdx.x == kCtlThread)
-    __hip_atomic_fetch_add(A.ctl + C_ARRIVED + (blockIdx.x % kSpread) * kLine, 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    arrived = __hip_atomic_fetch_add(A.ctl + C_ARRIVED + (blockIdx.x % kSpread) * kLine, 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
 
   if (router) {
     // the trace keeps one record per expert: XCD 0's task of its first tokens
@@ -951,7 +922,26 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     if (t >= n_tasks) break;
     const KA FusedArgs* Ai = Ap;
     asm volatile("" : "+s"(Ai));
-    run_task(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), epoch, troute);
+    run_task(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
+  }
+  // Two-level arrival count: the workgroup that completes its counter (of the
+  // workgroups b with the same b % kSpread) adds to C_ARRIVED2, and the one that
+  // completes that is the launch's last: it clears the counters and advances
+  // the epoch for the next launch.
+  if (wave == kWaves - 1) {
+    const int l = lane();
+    const uint32_t grp = blockIdx.x % kSpread;
+    const uint32_t in_grp = (gridDim.x - grp + kSpread - 1) / kSpread;
+    const uint32_t groups = gridDim.x < (uint32_t)kSpread ? gridDim.x : (uint32_t)kSpread;
+    if (shfl(arrived, 0) + 1u == in_grp) {
+      uint32_t old = 0u;
+      if (l == 0) old = __hip_atomic_fetch_add(A.ctl + C_ARRIVED2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (shfl(old, 0) + 1u == groups && l < kSpread) {
+        st_word(A.ctl + C_ARRIVED + l * kLine, 0u);
+        if (l == 0) st_word(A.ctl + C_ARRIVED2, 0u);
+        st_word(A.ctl + C_EPOCH + l * kLine, epoch + 1u);
+      }
+    }
   }
 }
 
