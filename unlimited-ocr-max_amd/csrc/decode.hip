@@ -24,8 +24,11 @@
 //   comb    64 columns, one token: shared-down partials -> sh, then the
 //           weighted combine of the token's routed rows plus sh        (H/64 x B)
 // The sgu tasks need no routing: a wave runs those while the routing is
-// computed.  The tasks that wait for other tasks' results (sfold, sdn, comb)
-// come last, so that no routed task is queued behind such a wait.  A routed task holds every chunk of its columns, so
+// computed.  The shared folds and down partials, which wait for the sgu
+// partials, come after the routed gate/up tasks, so that no routed gate/up
+// task is queued behind such a wait, but before the routed down tasks: their
+// inputs are long ready when a wave reaches them, and the combine, which waits
+// for them, is not kept waiting at the end.  A routed task holds every chunk of its columns, so
 // its per-group fold runs
 // inside the wave (lane shuffles); only the shared experts, whose chunks are
 // spread over tasks, fold partials written by other waves.  Each lane loads
@@ -158,31 +161,40 @@ __device__ __forceinline__ bool poll_done(bool ready, uint32_t& spin, uint32_t* 
 __device__ __forceinline__ bool expired(uint32_t spin) { return spin == 0u; }
 
 // Polls n tagged pairs p[i * stride] (i < n <= N, per lane) until all carry
-// `tag`; their values land in v[0..n).  It first probes only the first pair
-// of every lane, so a waiting wave reads one pair per lane per round instead
-// of n; the addresses advance from p (no per-index offsets for the compiler
+// `tag`; their values land in v[0..n).  A round trip is about a microsecond
+// under the weight streams.  Eager (inputs likely there already, as for the
+// routed down tasks at 8 tokens): the first round loads all n pairs, one round
+// trip when they are there.  Otherwise (and after an eager round found some
+// missing) each lane probes a single pair until it arrives and then reloads
+// the set: the many waves of a long wait (the routed down tasks at one token)
+// keep their reads light, which the weight streams they share the memory with
+// need.  The addresses advance from p (no per-index offsets for the compiler
 // to hoist out of the task loop).
 template <int N>
+__device__ __forceinline__ bool load_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, float (&v)[N]) {
+  uint64_t q[N];
+  const uint64_t* a = p;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = ld_pair(a);
+    if (i + 1 < n) a += stride;
+  }
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    v[i] = pair_value(q[i]);
+    ok = ok && pair_has(q[i], tag);
+  }
+  return ok;
+}
+template <int N, bool EAGER = false>
 __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, uint32_t* ctl,
                                            uint32_t limit, float (&v)[N]) {
   uint32_t spin = limit;
+  if (EAGER && __all(load_pairs<N>(p, stride, n, tag, v))) return;
   while (!poll_done(pair_has(ld_pair(p), tag), spin, ctl)) {
   }
-  for (;;) {
-    uint64_t q[N];
-    const uint64_t* a = p;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      q[i] = ld_pair(a);
-      if (i + 1 < n) a += stride;
-    }
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      v[i] = pair_value(q[i]);
-      ok = ok && pair_has(q[i], tag);
-    }
-    if (poll_done(ok, spin, ctl)) break;
+  while (!poll_done(load_pairs<N>(p, stride, n, tag, v), spin, ctl)) {
   }
   if (expired(spin)) {
 #pragma unroll
@@ -204,7 +216,7 @@ constexpr bool kTrace = UOCR_DECODE_TRACE != 0;
 
 // Phase timestamps of a task (the constant-rate wall clock), when tracing:
 // 0 start, 1 weights landed (waited for only when tracing), 3 inputs polled,
-// 4 chains done, 2 end, 5 when the wave learnt the routing, 7 the wave.
+// 4 chains done, 2 end, 5 when the wave learnt the routing, 6 the task kind, 7 the wave.
 #define UOCR_TRACE(a, task, slot)                                                                          \
   do {                                                                                                     \
     if (kTrace && (a).trace != nullptr && lane() == 0) (a).trace[(int64_t)(task) * 8 + (slot)] = (int64_t)wall_clock64(); \
@@ -234,12 +246,10 @@ __device__ __forceinline__ int task_count(const KA FusedArgs& A, int ng) {
 
 // Tasks before the routed ones: the router, and the shared gate/up partials
 // (which wait for nothing).  The shared folds and down partials, which wait
-// for other tasks, come after the routed tasks, so that a wave's routed work
-// is never queued behind such a wait: a wave's second task is then one whose
-// inputs come late anyway.
+// for the sgu partials, follow the routed gate/up tasks.
 __device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.E + A.n_sgu; }
 
-// Task order: router, sgu, rgu, rdn, sfold, sdn, comb (every task waits only
+// Task order: router, sgu, rgu, sfold, sdn, rdn, comb (every task waits only
 // for tasks before it).
 __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
   if (t < A.E) return {K_ROUTER, t, 0, 0};
@@ -257,11 +267,6 @@ __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
     return {K_RGU, s, t - s * A.per_e_gu, 0};
   }
   t -= ng * A.per_e_gu;
-  if (t < ng * A.per_e_dn) {
-    const int s = t / A.per_e_dn;
-    return {K_RDN, s, t - s * A.per_e_dn, 0};
-  }
-  t -= ng * A.per_e_dn;
   if (t < A.n_sfold) {
     const int u = t / A.B;
     return {K_SFOLD, u, t - u * A.B, 0};
@@ -272,6 +277,11 @@ __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
     return {K_SDN, cb, t - cb * A.gfs, 0};
   }
   t -= A.n_sdn;
+  if (t < ng * A.per_e_dn) {
+    const int s = t / A.per_e_dn;
+    return {K_RDN, s, t - s * A.per_e_dn, 0};
+  }
+  t -= ng * A.per_e_dn;
   if (t < A.n_comb) {
     const int cb = t / A.B;
     return {K_COMB, cb, t - cb * A.B, 0};
@@ -711,7 +721,8 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     const uint64_t* src = A.h + (int64_t)r * A.F + l;
     for (int i0 = 0; i0 < npairs; i0 += kMaxP) {
       float v[kMaxP];
-      poll_pairs<kMaxP>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl, A.spin_limit, v);
+      poll_pairs<kMaxP, true>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl, A.spin_limit,
+                              v);
 #pragma unroll
       for (int i = 0; i < kMaxP; ++i) {
         if (i0 + i < npairs) {
@@ -773,7 +784,10 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
   Ctx C = C0;
   C.t = t;
   UOCR_TRACE(A, t, 0);
-  if (kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)t * 8 + 5] = troute;
+  if (kTrace && A.trace != nullptr && lane() == 0) {
+    A.trace[(int64_t)t * 8 + 5] = troute;
+    A.trace[(int64_t)t * 8 + 6] = k.kind;
+  }
   switch (k.kind) {
     case K_SGU: task_sgu(A, C, k); break;
     case K_RGU:
