@@ -162,14 +162,16 @@ __device__ __forceinline__ bool expired(uint32_t spin) { return spin == 0u; }
 
 // Polls n tagged pairs p[i * stride] (i < n <= N, per lane) until all carry
 // `tag`; their values land in v[0..n).  A round trip is about a microsecond
-// under the weight streams.  Eager (inputs likely there already, as for the
-// routed down tasks at 8 tokens): the first round loads all n pairs, one round
-// trip when they are there.  Otherwise (and after an eager round found some
-// missing) each lane probes a single pair until it arrives and then reloads
-// the set: the many waves of a long wait (the routed down tasks at one token)
-// keep their reads light, which the weight streams they share the memory with
-// need.  The addresses advance from p (no per-index offsets for the compiler
-// to hoist out of the task loop).
+// under the weight streams.  kPollProbe: each lane probes a single pair
+// (`probe`, else the first) until it arrives, then loads the set until it is
+// complete: the many waves of a long wait keep their reads light, which the
+// weight streams they share the memory with need.  kPollEager: when `eager`,
+// a first round loads the whole set (one round trip when it is there
+// already), then as kPollProbe.  kPollFull: every round loads the set (one
+// round trip after the last pair lands; for the few waves of the combine).
+// The addresses advance from p (no per-index offsets for the compiler to
+// hoist out of the task loop).
+enum : int { kPollProbe = 0, kPollEager = 1, kPollFull = 2 };
 template <int N>
 __device__ __forceinline__ bool load_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, float (&v)[N]) {
   uint64_t q[N];
@@ -187,12 +189,16 @@ __device__ __forceinline__ bool load_pairs(const uint64_t* p, int64_t stride, in
   }
   return ok;
 }
-template <int N, bool EAGER = false>
+template <int N, int MODE = kPollProbe>
 __device__ __forceinline__ void poll_pairs(const uint64_t* p, int64_t stride, int n, uint32_t tag, uint32_t* ctl,
-                                           uint32_t limit, float (&v)[N]) {
+                                           uint32_t limit, float (&v)[N], const uint64_t* probe = nullptr,
+                                           bool eager = true) {
   uint32_t spin = limit;
-  if (EAGER && __all(load_pairs<N>(p, stride, n, tag, v))) return;
-  while (!poll_done(pair_has(ld_pair(p), tag), spin, ctl)) {
+  if (MODE == kPollEager && eager && __all(load_pairs<N>(p, stride, n, tag, v))) return;
+  if (MODE != kPollFull) {
+    if (probe == nullptr) probe = p;
+    while (!poll_done(pair_has(ld_pair(probe), tag), spin, ctl)) {
+    }
   }
   while (!poll_done(load_pairs<N>(p, stride, n, tag, v), spin, ctl)) {
   }
@@ -652,16 +658,17 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
   const int ncols = min(A.c_gu, A.F - n0);
   Stage<INT8> st;
   issue_routed<INT8>(A, true, e, n0, ncols, st);
-  UOCR_TRACE_LOADS(A, C.t);
   const int lanes = 2 * ncols * A.gh;
   const int lam = min(l, lanes - 1);
   const int cp = small_div(lam, A.inv_gh);
   const int g = lam - cp * A.gh;
   const int c = cp >> 1;
   const int base = cp * A.gh;  // first lane of the lane's (column, projection)
+  float scale = 0.0f;
+  if constexpr (INT8) scale = ldg(((cp & 1) ? A.up_s : A.gate_s) + ((int64_t)e * A.F + n0 + c) * A.gh + g);
+  UOCR_TRACE_LOADS(A, C.t);
   float sv[INT8 ? kMaxG : 1];
   if constexpr (INT8) {
-    const float scale = ldg(((cp & 1) ? A.up_s : A.gate_s) + ((int64_t)e * A.F + n0 + c) * A.gh + g);
 #pragma unroll
     for (int gg = 0; gg < kMaxG; ++gg) sv[gg] = shfl(scale, base + min(gg, A.gh - 1));
   }
@@ -694,7 +701,7 @@ template <bool INT8>
 __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
-  constexpr int kMaxP = 8;  // pairs per lane per poll round
+  constexpr int kMaxP = 16;  // pairs per lane per poll round (F <= 1024 in one round)
   const int l = lane();
   const int e = slot_expert(rt, k.a);
   uint64_t rows = slot_rows(rt, e);
@@ -702,15 +709,16 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   const int ncols = min(A.c_dn, A.H - n0);
   Stage<INT8> st;
   issue_routed<INT8>(A, false, e, n0, ncols, st);
-  UOCR_TRACE_LOADS(A, C.t);
   const int lanes = ncols * A.gf;
   const int lam = min(l, lanes - 1);
   const int c = small_div(lam, A.inv_gf);
   const int g = lam - c * A.gf;
   const int base = c * A.gf;
+  float scale = 0.0f;
+  if constexpr (INT8) scale = ldg(A.down_s + ((int64_t)e * A.H + n0 + c) * A.gf + g);
+  UOCR_TRACE_LOADS(A, C.t);
   float sv[INT8 ? kMaxG : 1];
   if constexpr (INT8) {
-    const float scale = ldg(A.down_s + ((int64_t)e * A.H + n0 + c) * A.gf + g);
 #pragma unroll
     for (int gg = 0; gg < kMaxG; ++gg) sv[gg] = shfl(scale, base + min(gg, A.gf - 1));
   }
@@ -721,8 +729,15 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     const uint64_t* src = A.h + (int64_t)r * A.F + l;
     for (int i0 = 0; i0 < npairs; i0 += kMaxP) {
       float v[kMaxP];
-      poll_pairs<kMaxP, true>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl, A.spin_limit,
-                              v);
+      // The probe is the row's last pair (its columns come from the expert's
+      // last gate/up tasks).  The whole set is tried first only when the
+      // wave's previous task (this one's index less the wave count) came
+      // after every routed gate/up task: all of them have then been running
+      // for at least a task's time, and h is likely there.  Otherwise (every
+      // down task at one token) the eager round would only add traffic.
+      poll_pairs<kMaxP, kPollEager>(src + (int64_t)i0 * kWave, kWave, min(kMaxP, npairs - i0), C.tag, A.ctl,
+                                    A.spin_limit, v, src + (int64_t)(npairs - 1) * kWave,
+                                    C.t - (int)gridDim.x * kWaves >= unrouted_count(A) + rt.ng * A.per_e_gu);
 #pragma unroll
       for (int i = 0; i < kMaxP; ++i) {
         if (i0 + i < npairs) {
@@ -769,7 +784,7 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   for (int g = 0; g < kMaxG; ++g)
     if (g < A.gfs) shv = shv + v[g];
   float y[kMaxK];
-  poll_pairs<kMaxK>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, A.spin_limit, y);
+  poll_pairs<kMaxK, kPollFull>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, A.spin_limit, y);
   UOCR_TRACE(A, C.t, 3);
   float acc = 0.0f;
 #pragma unroll
