@@ -365,8 +365,13 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
     // the selected probabilities summed in selection order, then divided
     float* ws = (float*)(keys + kWave);
     if (chosen) ws[rank] = pr;
+    float wv[8];  // topk <= 8
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[j] = ws[min(j, A.topk - 1)];
     float d = 0.0f;
-    for (int j = 0; j < A.topk; ++j) d = d + ws[j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < A.topk) d = d + wv[j];
     my_w = pr / d;
   }
   if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 5] = (int64_t)wall_clock64();
@@ -544,6 +549,8 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
   const int nk = A.H / kWave;
   for (int t = t0; t < t1; ++t) {
     const float* xr = C.xs + t * A.gh * kXPad + l;
+    // (issuing every read before the chain made the layer slower at one
+    // token, though the chain itself got shorter)
     float p = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxJ; ++j)
@@ -644,6 +651,34 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   }
 }
 
+// The fold of a column's G group partials (lanes base .. base+G-1) in group
+// order: acc = fma(scale_g, partial_g, acc) from 0 (int8), or the plain sum
+// (bf16).  Every shuffle is issued before the first add (a shuffle under the
+// loop's bound would wait for each one in turn).
+template <bool INT8, int MAXG>
+__device__ __forceinline__ float fold_groups(float part, int base, int G, const float (&sv)[INT8 ? MAXG : 1]) {
+  constexpr int kBatch = 8;  // shuffles in flight (registers)
+  float acc = 0.0f;
+#pragma unroll
+  for (int g0 = 0; g0 < MAXG; g0 += kBatch) {
+    if (g0 < G) {
+      float pv[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) pv[i] = shfl(part, base + min(g0 + i, G - 1));
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (g0 + i < G) {
+          if constexpr (INT8)
+            acc = __builtin_fmaf(sv[g0 + i], pv[i], acc);
+          else
+            acc = acc + pv[i];
+        }
+      }
+    }
+  }
+  return acc;
+}
+
 // Routed gate+up of one expert for c_gu columns, every chunk of H, the
 // expert's routed rows: h = silu(fold(gate)) * fold(up), fold over the
 // 128-groups in order.
@@ -678,17 +713,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
     rows &= rows - 1ull;
     launder(st);
     const float part = chain<INT8>(st, C.xs + ((r / A.topk) * A.gh + g) * kXPad);
-    float acc = 0.0f;
-#pragma unroll
-    for (int gg = 0; gg < kMaxG; ++gg) {
-      if (gg < A.gh) {
-        const float pv = shfl(part, base + gg);
-        if constexpr (INT8)
-          acc = __builtin_fmaf(sv[gg], pv, acc);
-        else
-          acc = acc + pv;
-      }
-    }
+    const float acc = fold_groups<INT8, kMaxG>(part, base, A.gh, sv);
     UOCR_TRACE(A, C.t, 4);
     const float up = shfl(acc, min(l + A.gh, kWave - 1));
     if (writer) st_pair(A.h + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
@@ -750,17 +775,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     UOCR_TRACE(A, C.t, 3);
     launder(st);
     const float part = chain<INT8>(st, C.act + g * kXPad);
-    float acc = 0.0f;
-#pragma unroll
-    for (int gg = 0; gg < kMaxG; ++gg) {
-      if (gg < A.gf) {
-        const float pv = shfl(part, base + gg);
-        if constexpr (INT8)
-          acc = __builtin_fmaf(sv[gg], pv, acc);
-        else
-          acc = acc + pv;
-      }
-    }
+    const float acc = fold_groups<INT8, kMaxG>(part, base, A.gf, sv);
     UOCR_TRACE(A, C.t, 4);
     if (g == 0 && l < lanes) st_pair(A.y + (int64_t)r * A.H + n0 + c, acc, C.tag);
     __builtin_amdgcn_wave_barrier();
@@ -786,14 +801,18 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   float y[kMaxK];
   poll_pairs<kMaxK, kPollFull>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, A.spin_limit, y);
   UOCR_TRACE(A, C.t, 3);
+  float wj[kMaxK];
+#pragma unroll
+  for (int j = 0; j < kMaxK; ++j) wj[j] = C.r_wts[t * A.topk + min(j, A.topk - 1)];
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j)
-    if (j < A.topk) acc = __builtin_fmaf(C.r_wts[t * A.topk + j], y[j], acc);
+    if (j < A.topk) acc = __builtin_fmaf(wj[j], y[j], acc);
   A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : acc + shv;
 }
 
-// Runs task t.
+// Runs task t (INT8: the routed experts' weights are int8 with scales).
+template <bool INT8>
 __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, const Ctx& C0, const Route& rt, int t,
                                                         const Task& k, int64_t troute) {
   Ctx C = C0;
@@ -805,20 +824,10 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
   }
   switch (k.kind) {
     case K_SGU: task_sgu(A, C, k); break;
-    case K_RGU:
-      if (A.int8)
-        task_rgu<true>(A, C, rt, k);
-      else
-        task_rgu<false>(A, C, rt, k);
-      break;
+    case K_RGU: task_rgu<INT8>(A, C, rt, k); break;
     case K_SFOLD: task_sfold(A, C, k); break;
     case K_SDN: task_sdn(A, C, k); break;
-    case K_RDN:
-      if (A.int8)
-        task_rdn<true>(A, C, rt, k);
-      else
-        task_rdn<false>(A, C, rt, k);
-      break;
+    case K_RDN: task_rdn<INT8>(A, C, rt, k); break;
     case K_COMB: task_comb(A, C, k); break;
     default: break;
   }
@@ -827,6 +836,9 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
     A.trace[(int64_t)t * 8 + 7] = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
 }
 
+// One instantiation per routed weight type, each with its own register
+// allocation (the bf16 stage is twice the int8 one).
+template <bool INT8>
 __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   (void)args;  // read in place, through the kernel-argument segment
   const KA FusedArgs* Ap = (const KA FusedArgs*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -919,6 +931,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     const bool traced = r_t0 == 0 && blockIdx.x % kXcds == 0;
     C.t = r_e;
     if (traced) UOCR_TRACE(A, r_e, 0);
+    if (traced) UOCR_TRACE_LOADS(A, r_e);
     router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
     if (traced) UOCR_TRACE(A, r_e, 2);
     if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
@@ -951,7 +964,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     if (t >= n_tasks) break;
     const KA FusedArgs* Ai = Ap;
     asm volatile("" : "+s"(Ai));
-    run_task(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
+    run_task<INT8>(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
   }
   // Two-level arrival count: the workgroup that completes its counter (of the
   // workgroups b with the same b % kSpread) adds to C_ARRIVED2, and the one that
@@ -1017,15 +1030,19 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
 
 bool fused_trace_built() { return kTrace; }
 
+// The resident capacity of both instantiations (the smaller, so that one
+// grid suits either).
 hipError_t fused_grid(size_t lds_bytes, int* grid) {
-  int dev = 0, cus = 0, per_cu = 0;
+  int dev = 0, cus = 0, per_cu[2] = {0, 0};
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute((const void*)k_decode_fused, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode_fused, kThreads, lds_bytes);
+  const void* kernels[2] = {(const void*)k_decode_fused<true>, (const void*)k_decode_fused<false>};
+  for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+    e = hipFuncSetAttribute(kernels[i], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu[i], kernels[i], kThreads, lds_bytes);
+  }
   if (e != hipSuccess) return e;
-  *grid = cus * per_cu;
+  *grid = cus * (per_cu[0] < per_cu[1] ? per_cu[0] : per_cu[1]);
   return hipSuccess;
 }
 
@@ -1034,7 +1051,10 @@ hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, h
   if (grid % kXcds != 0 || a.r_tok < 1 ||
       (int64_t)(grid / kXcds) * kRouterWaves < (int64_t)a.E * ((a.B + a.r_tok - 1) / a.r_tok))
     return hipErrorInvalidConfiguration;
-  UOCR_LAUNCH("decode_fused", k_decode_fused, dim3(grid), dim3(kThreads), lds_bytes, s, a);
+  if (a.int8)
+    UOCR_LAUNCH("decode_fused", k_decode_fused<true>, dim3(grid), dim3(kThreads), lds_bytes, s, a);
+  else
+    UOCR_LAUNCH("decode_fused", k_decode_fused<false>, dim3(grid), dim3(kThreads), lds_bytes, s, a);
   return hipGetLastError();
 }
 
