@@ -652,24 +652,29 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
 }
 
 // The fold of a column's G group partials (lanes base .. base+G-1) in group
-// order: acc = fma(scale_g, partial_g, acc) from 0 (int8), or the plain sum
-// (bf16).  Every shuffle is issued before the first add (a shuffle under the
-// loop's bound would wait for each one in turn).
+// order: acc = fma(scale_g, partial_g, acc) from 0 (int8, scale_g in the same
+// lane as partial_g), or the plain sum (bf16).  Every shuffle of a batch is
+// issued before its first add (a shuffle under the loop's bound would wait for
+// each one in turn).
 template <bool INT8, int MAXG>
-__device__ __forceinline__ float fold_groups(float part, int base, int G, const float (&sv)[INT8 ? MAXG : 1]) {
+__device__ __forceinline__ float fold_groups(float part, float scale, int base, int G) {
   constexpr int kBatch = 8;  // shuffles in flight (registers)
   float acc = 0.0f;
 #pragma unroll
   for (int g0 = 0; g0 < MAXG; g0 += kBatch) {
     if (g0 < G) {
-      float pv[kBatch];
+      float pv[kBatch], sv[INT8 ? kBatch : 1];
 #pragma unroll
-      for (int i = 0; i < kBatch; ++i) pv[i] = shfl(part, base + min(g0 + i, G - 1));
+      for (int i = 0; i < kBatch; ++i) {
+        const int src = base + min(g0 + i, G - 1);
+        pv[i] = shfl(part, src);
+        if constexpr (INT8) sv[i] = shfl(scale, src);
+      }
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         if (g0 + i < G) {
           if constexpr (INT8)
-            acc = __builtin_fmaf(sv[g0 + i], pv[i], acc);
+            acc = __builtin_fmaf(sv[i], pv[i], acc);
           else
             acc = acc + pv[i];
         }
@@ -679,50 +684,75 @@ __device__ __forceinline__ float fold_groups(float part, int base, int G, const 
   return acc;
 }
 
-// Routed gate+up of one expert for c_gu columns, every chunk of H, the
-// expert's routed rows: h = silu(fold(gate)) * fold(up), fold over the
-// 128-groups in order.
-template <bool INT8>
+// Column blocks of a routed task: SUB blocks of c columns from column
+// (task index) * SUB * c; a block past the last column is empty (ncols <= 0)
+// and neither loads nor computes.  Every block's weights are loaded before
+// the first is computed, so a wave waits for its weights once per SUB blocks.
+template <bool INT8, int SUB>
+struct Blocks {
+  Stage<INT8> st[SUB];
+  float scale[SUB];
+  int n0[SUB], ncols[SUB];
+};
+
+// Routed gate+up of one expert for SUB blocks of c_gu columns, every chunk of
+// H, the expert's routed rows: h = silu(fold(gate)) * fold(up), fold over the
+// 128-groups in order.  Lane l of a block is (column, projection, group) =
+// ((2c + p) * gh + g).
+template <bool INT8, int SUB>
 __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
   const int l = lane();
   const int e = slot_expert(rt, k.a);
-  uint64_t rows = slot_rows(rt, e);
-  const int n0 = k.b * A.c_gu;
-  const int ncols = min(A.c_gu, A.F - n0);
-  Stage<INT8> st;
-  issue_routed<INT8>(A, true, e, n0, ncols, st);
-  const int lanes = 2 * ncols * A.gh;
-  const int lam = min(l, lanes - 1);
-  const int cp = small_div(lam, A.inv_gh);
-  const int g = lam - cp * A.gh;
-  const int c = cp >> 1;
-  const int base = cp * A.gh;  // first lane of the lane's (column, projection)
-  float scale = 0.0f;
-  if constexpr (INT8) scale = ldg(((cp & 1) ? A.up_s : A.gate_s) + ((int64_t)e * A.F + n0 + c) * A.gh + g);
-  UOCR_TRACE_LOADS(A, C.t);
-  float sv[INT8 ? kMaxG : 1];
-  if constexpr (INT8) {
+  const uint64_t rows0 = slot_rows(rt, e);
+  Blocks<INT8, SUB> bk;
 #pragma unroll
-    for (int gg = 0; gg < kMaxG; ++gg) sv[gg] = shfl(scale, base + min(gg, A.gh - 1));
+  for (int j = 0; j < SUB; ++j) {
+    bk.n0[j] = (k.b * SUB + j) * A.c_gu;
+    bk.ncols[j] = min(A.c_gu, A.F - bk.n0[j]);
+    bk.scale[j] = 0.0f;
+    if (bk.ncols[j] > 0) {
+      issue_routed<INT8>(A, true, e, bk.n0[j], bk.ncols[j], bk.st[j]);
+      if constexpr (INT8) {
+        const int lam = min(l, 2 * bk.ncols[j] * A.gh - 1);
+        const int cp = small_div(lam, A.inv_gh);
+        bk.scale[j] = ldg(((cp & 1) ? A.up_s : A.gate_s) + ((int64_t)e * A.F + bk.n0[j] + (cp >> 1)) * A.gh +
+                          (lam - cp * A.gh));
+      }
+    }
   }
-  const bool writer = (cp & 1) == 0 && g == 0 && l < lanes;
-  while (rows != 0ull) {
-    const int r = (int)__builtin_ctzll(rows);
-    rows &= rows - 1ull;
-    launder(st);
-    const float part = chain<INT8>(st, C.xs + ((r / A.topk) * A.gh + g) * kXPad);
-    const float acc = fold_groups<INT8, kMaxG>(part, base, A.gh, sv);
-    UOCR_TRACE(A, C.t, 4);
-    const float up = shfl(acc, min(l + A.gh, kWave - 1));
-    if (writer) st_pair(A.h + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
+  UOCR_TRACE_LOADS(A, C.t);
+#pragma unroll
+  for (int j = 0; j < SUB; ++j) {
+    if (bk.ncols[j] <= 0) break;
+    const int n0 = bk.n0[j];
+    const int lanes = 2 * bk.ncols[j] * A.gh;
+    const int lam = min(l, lanes - 1);
+    const int cp = small_div(lam, A.inv_gh);
+    const int g = lam - cp * A.gh;
+    const int c = cp >> 1;
+    const int base = cp * A.gh;  // first lane of the lane's (column, projection)
+    const bool writer = (cp & 1) == 0 && g == 0 && l < lanes;
+    uint64_t rows = rows0;
+    while (rows != 0ull) {
+      const int r = (int)__builtin_ctzll(rows);
+      rows &= rows - 1ull;
+      launder(bk.st[j]);
+      const float part = chain<INT8>(bk.st[j], C.xs + ((r / A.topk) * A.gh + g) * kXPad);
+      const float acc = fold_groups<INT8, kMaxG>(part, bk.scale[j], base, A.gh);
+      UOCR_TRACE(A, C.t, 4);
+      const float up = shfl(acc, min(l + A.gh, kWave - 1));
+      if (writer) st_pair(A.h + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
+    }
   }
 }
 
-// Routed down of one expert for c_dn columns, every chunk of F, row by row:
-// y = fold over the 128-groups in order.
-template <bool INT8>
+// Routed down of one expert for SUB blocks of c_dn columns, every chunk of F,
+// row by row: y = fold over the 128-groups in order.  Lane l of a block is
+// (column, group of F) = (c * gf + g).  A row of h is polled once for all
+// blocks.
+template <bool INT8, int SUB>
 __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
@@ -730,23 +760,22 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   const int l = lane();
   const int e = slot_expert(rt, k.a);
   uint64_t rows = slot_rows(rt, e);
-  const int n0 = k.b * A.c_dn;
-  const int ncols = min(A.c_dn, A.H - n0);
-  Stage<INT8> st;
-  issue_routed<INT8>(A, false, e, n0, ncols, st);
-  const int lanes = ncols * A.gf;
-  const int lam = min(l, lanes - 1);
-  const int c = small_div(lam, A.inv_gf);
-  const int g = lam - c * A.gf;
-  const int base = c * A.gf;
-  float scale = 0.0f;
-  if constexpr (INT8) scale = ldg(A.down_s + ((int64_t)e * A.H + n0 + c) * A.gf + g);
-  UOCR_TRACE_LOADS(A, C.t);
-  float sv[INT8 ? kMaxG : 1];
-  if constexpr (INT8) {
+  Blocks<INT8, SUB> bk;
 #pragma unroll
-    for (int gg = 0; gg < kMaxG; ++gg) sv[gg] = shfl(scale, base + min(gg, A.gf - 1));
+  for (int j = 0; j < SUB; ++j) {
+    bk.n0[j] = (k.b * SUB + j) * A.c_dn;
+    bk.ncols[j] = min(A.c_dn, A.H - bk.n0[j]);
+    bk.scale[j] = 0.0f;
+    if (bk.ncols[j] > 0) {
+      issue_routed<INT8>(A, false, e, bk.n0[j], bk.ncols[j], bk.st[j]);
+      if constexpr (INT8) {
+        const int lam = min(l, bk.ncols[j] * A.gf - 1);
+        const int c = small_div(lam, A.inv_gf);
+        bk.scale[j] = ldg(A.down_s + ((int64_t)e * A.H + bk.n0[j] + c) * A.gf + (lam - c * A.gf));
+      }
+    }
   }
+  UOCR_TRACE_LOADS(A, C.t);
   const int npairs = A.F / kWave;  // pairs of one h row per lane: element l + 64 i
   while (rows != 0ull) {
     const int r = (int)__builtin_ctzll(rows);
@@ -773,11 +802,19 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     }
     __builtin_amdgcn_wave_barrier();
     UOCR_TRACE(A, C.t, 3);
-    launder(st);
-    const float part = chain<INT8>(st, C.act + g * kXPad);
-    const float acc = fold_groups<INT8, kMaxG>(part, base, A.gf, sv);
-    UOCR_TRACE(A, C.t, 4);
-    if (g == 0 && l < lanes) st_pair(A.y + (int64_t)r * A.H + n0 + c, acc, C.tag);
+#pragma unroll
+    for (int j = 0; j < SUB; ++j) {
+      if (bk.ncols[j] <= 0) break;
+      const int lanes = bk.ncols[j] * A.gf;
+      const int lam = min(l, lanes - 1);
+      const int c = small_div(lam, A.inv_gf);
+      const int g = lam - c * A.gf;
+      launder(bk.st[j]);
+      const float part = chain<INT8>(bk.st[j], C.act + g * kXPad);
+      const float acc = fold_groups<INT8, kMaxG>(part, bk.scale[j], c * A.gf, A.gf);
+      UOCR_TRACE(A, C.t, 4);
+      if (g == 0 && l < lanes) st_pair(A.y + (int64_t)r * A.H + bk.n0[j] + c, acc, C.tag);
+    }
     __builtin_amdgcn_wave_barrier();
   }
 }
@@ -824,10 +861,15 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
   }
   switch (k.kind) {
     case K_SGU: task_sgu(A, C, k); break;
-    case K_RGU: task_rgu<INT8>(A, C, rt, k); break;
+    case K_RGU:
+      if (INT8 && A.sub == 2)
+        task_rgu<INT8, 2>(A, C, rt, k);
+      else
+        task_rgu<INT8, 1>(A, C, rt, k);
+      break;
     case K_SFOLD: task_sfold(A, C, k); break;
     case K_SDN: task_sdn(A, C, k); break;
-    case K_RDN: task_rdn<INT8>(A, C, rt, k); break;
+    case K_RDN: task_rdn<INT8, 1>(A, C, rt, k); break;
     case K_COMB: task_comb(A, C, k); break;
     default: break;
   }
@@ -989,14 +1031,17 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
 
 }  // namespace
 
-FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk) {
+int fused_sub(bool int8, int B) { return int8 && B >= kFusedSubRows ? 2 : 1; }
+
+FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk, int sub) {
   FusedLayout L{};
   L.gh = H / 128;
   L.gf = F / 128;
   L.gfs = Fs / 128;
+  L.sub = sub;
   L.c_gu = L.gh > 0 ? 64 / (2 * L.gh) : 0;
   L.c_dn = L.gf > 0 ? 64 / L.gf : 0;
-  L.per_e_gu = L.c_gu > 0 ? (F + L.c_gu - 1) / L.c_gu : 0;
+  L.per_e_gu = L.c_gu > 0 ? (F + L.c_gu * sub - 1) / (L.c_gu * sub) : 0;
   L.per_e_dn = L.c_dn > 0 ? (H + L.c_dn - 1) / L.c_dn : 0;
   L.cb_fs = Fs / 64;
   L.cb_h = H / 64;

@@ -238,57 +238,67 @@ __global__ void __launch_bounds__(256) k_logits(float* __restrict__ logits, cons
 
 // ---------------------------------------------------------------- softmax + top-k
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
+// LDS words a wave's token_topk needs: 64 keys, then up to 64 selected
+// probabilities (as floats, 32 words).
+constexpr int kTopkScratch = 96;
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off, kWave);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-// One wave: softmax over the E <= 64 logits of one token and its top-k.
-// Lane 0 writes the results; returns nothing else.
+// One wave: softmax over the E <= 64 logits of one token and its top-k.  The
+// max and the sum are the halving trees (the sum's additions in the order of
+// wave_tree_sum); the k largest probabilities in turn, ties to the lower id,
+// as ranks: lane l's key (bits of p) << 32 | (64 - l) is distinct and orders
+// the lanes by probability then lower id, so the j-th selection is the lane
+// with j larger keys, counted over the 64 keys in `scratch` (kTopkScratch
+// words of this wave's LDS).  The chosen lanes write their slot; with renorm
+// the weights are divided by their sum taken in selection order.
 __device__ void token_topk(const float* __restrict__ lrow, int E, int topk, int renorm, int32_t* ids32,
-                           int64_t* ids64, float* wts, int32_t* lds_ids) {
+                           int64_t* ids64, float* wts, int32_t* lds_ids, uint64_t* scratch) {
   const int l = lane_id();
   const float v = l < E ? lrow[l] : -__builtin_huge_valf();
-  const float m = wave_max(v);
+  const float m = tree_max(v);
   const float ex = l < E ? uexp(v - m) : 0.0f;
-  const float S = __shfl(wave_tree_sum(ex), 0, kWave);
+  const float S = tree_sum(ex);
   const float p = l < E ? ex / S : 0.0f;
-  uint64_t key = l < E ? (((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(kWave - l)) : 0ull;
-  float d = 0.0f;  // the renormaliser, summed in selection order
-  for (int j = 0; j < topk; ++j) {
-    const uint64_t best = wave_max_u64(key);
-    const int sel = kWave - (int)(best & 0xFFFFFFFFu);
-    const float ws = __shfl(p, sel, kWave);
-    d = d + ws;
-    if (l == sel) key = 0ull;
-    if (l == 0) {
-      if (ids32) ids32[j] = sel;
-      if (ids64) ids64[j] = sel;
-      if (wts) wts[j] = ws;
-      if (lds_ids) lds_ids[j] = sel;
-    }
+  const uint64_t key = l < E ? (((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(kWave - l)) : 0ull;
+  scratch[l] = key;
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < kWave; j += 2) {
+    const u64x2 kk = *(const u64x2*)(scratch + j);
+    rank += (kk[0] > key ? 1 : 0) + (kk[1] > key ? 1 : 0);
   }
-  if (renorm && wts && l == 0)
-    for (int j = 0; j < topk; ++j) wts[j] = wts[j] / d;
+  const bool chosen = l < E && rank < topk;
+  float w = p;
+  if (renorm) {
+    float* sel = (float*)(scratch + kWave);
+    if (chosen) sel[rank] = p;
+    float d = 0.0f;  // the renormaliser, summed in selection order
+    for (int j0 = 0; j0 < topk; j0 += 8) {
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = sel[min(j0 + i, topk - 1)];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (j0 + i < topk) d = d + sv[i];
+    }
+    w = p / d;
+  }
+  if (chosen) {
+    if (ids32) ids32[rank] = l;
+    if (ids64) ids64[rank] = l;
+    if (wts) wts[rank] = w;
+    if (lds_ids) lds_ids[rank] = l;
+  }
 }
 
 __global__ void __launch_bounds__(256) k_softmax_topk(const float* __restrict__ logits, int T, int E, int topk,
                                                       int renorm, int32_t* ids32, int64_t* ids64, float* wts) {
-  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  __shared__ uint64_t scratch[4][kTopkScratch];
+  const int w = (int)(threadIdx.x >> 6);
+  const int t = (int)blockIdx.x * 4 + w;
   if (t >= T) return;
   const int64_t o = (int64_t)t * topk;
   token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 ? ids32 + o : nullptr, ids64 ? ids64 + o : nullptr,
-             wts ? wts + o : nullptr, nullptr);
+             wts ? wts + o : nullptr, nullptr, scratch[w]);
 }
 
 // ---------------------------------------------------------------- grouping
@@ -442,6 +452,7 @@ __global__ void __launch_bounds__(kCountThreads) k_topk_count(const float* __res
                                                               float* __restrict__ wts, int32_t* __restrict__ total,
                                                               int32_t* __restrict__ base) {
   __shared__ int cnt[kRouteMaxExperts];
+  __shared__ uint64_t scratch[kCountTokens][kTopkScratch];
   const int b = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int t0 = b * kCountTokens;
@@ -450,7 +461,7 @@ __global__ void __launch_bounds__(kCountThreads) k_topk_count(const float* __res
   const int t = t0 + tid / kWave;
   if (t < t1) {
     const int64_t o = (int64_t)t * topk;
-    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, nullptr);
+    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, nullptr, scratch[tid / kWave]);
   }
   __syncthreads();  // the block's ids (global) are visible to the whole workgroup
   for (int64_t r = (int64_t)t0 * topk + tid; r < (int64_t)t1 * topk; r += kCountThreads)
@@ -522,38 +533,111 @@ __global__ void __launch_bounds__(kScatterThreads) k_group_scatter(const int32_t
 
 // ---------------------------------------------------------------- prefill routing, T below 2048
 //
-// k_logits_topk: a workgroup of 8 waves owns 4 tokens and every expert
-// (E <= 64): wave w computes the 4 tokens' logits of experts 8w .. 8w+7 (the
-// tile kernel's chains and trees: the same bits), then, after a barrier,
-// waves 0-3 run one token's softmax + top-k each, and the workgroup's rows per expert go to hist[b] (every expert,
-// zeros included).  k_group_scatter_hist: workgroup b sums hist over all
-// counting workgroups and over those before it, derives the tables
-// (workgroup 0 writes them) and places its rows.  No counters to clear.
+// k_logits_topk: a workgroup of 16 waves owns 4 tokens and every expert
+// (E <= 64).  Its x rows go to LDS (and to xb, rounded to bf16, when asked)
+// while each wave loads the router rows of its 4 experts (4w .. 4w+3) for
+// every k step at once: one memory latency for both.  Wave w then computes
+// the 4 tokens' logits of its experts (the tile kernel's chains over
+// k = lane + 64 j and its trees: the same bits) into LDS and the logits
+// buffer; after a barrier waves 0-3 run one token's softmax + top-k each, and
+// the workgroup's rows per expert go to hist[b] (every expert, zeros
+// included).  k_group_scatter_hist: workgroup b sums hist over all counting
+// workgroups and over those before it, derives the tables (workgroup 0
+// writes them) and places its rows.  No counters to clear.
 
 constexpr int kFusedTokens = 4;
+constexpr int kRouteWaves = 16;
+constexpr int kFusedSteps = 20;  // router k steps per batch (H <= 1280 in one batch)
 
-__global__ void __launch_bounds__(512) k_logits_topk(float* __restrict__ logits, uint16_t* __restrict__ xb,
-                                                     const float* __restrict__ x, int64_t ldx,
-                                                     const float* __restrict__ router, int T, int E, int H, int topk,
-                                                     int renorm, int32_t* __restrict__ ids32, float* __restrict__ wts,
-                                                     int32_t* __restrict__ hist) {
+__global__ void __launch_bounds__(kRouteWaves * 64) k_logits_topk(
+    float* __restrict__ logits, uint16_t* __restrict__ xb, const float* __restrict__ x, int64_t ldx,
+    const float* __restrict__ router, int T, int E, int H, int topk, int renorm, int32_t* __restrict__ ids32,
+    float* __restrict__ wts, int32_t* __restrict__ hist) {
+  __shared__ float xs[kFusedTokens * kLogitsMaxH];
+  __shared__ float lg[kFusedTokens][64];
   __shared__ int cnt[64];
   __shared__ int ids_lds[kFusedTokens * 64];
+  __shared__ uint64_t scratch[kFusedTokens][kTopkScratch];
   const int b = (int)blockIdx.x;
   const int w = (int)(threadIdx.x >> 6);
+  const int l = lane_id();
   const int tid = (int)threadIdx.x;
   const int t0 = b * kFusedTokens;
+  const int nt = min(kFusedTokens, T - t0);
+  const int nj = H / kWave;
+  const int e0 = 4 * w;
+  const bool active = e0 < E;
   if (tid < 64) cnt[tid] = 0;
-  logits_tile<kFusedTokens, 8>(logits, xb, x, ldx, router, T, E, H, t0, 8 * w, xb != nullptr && w == 0);
-  __syncthreads();  // the workgroup's logits (global) are visible to all its waves
-  const int t = t0 + w;
-  if (w < kFusedTokens && t < T) {
-    const int64_t o = (int64_t)t * topk;
-    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + w * topk);
+  // the first batch of router values, issued before the x rows are staged
+  const float* wl = router + (int64_t)min(e0, E - 1) * H + l;
+  int64_t wo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wo[e] = (int64_t)min(e, E - 1 - min(e0, E - 1)) * H;
+  float wa[kFusedSteps][4];
+  if (active) {
+#pragma unroll
+    for (int jj = 0; jj < kFusedSteps; ++jj)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wa[jj][e] = ldg(wl + wo[e] + min(jj, nj - 1) * kWave);
+  }
+  for (int i = tid; i < nt * H; i += kRouteWaves * kWave) {
+    const int t = i / H;
+    const int k = i - t * H;
+    const float v = ldg(x + (int64_t)(t0 + t) * ldx + k);
+    xs[t * H + k] = v;
+    if (xb != nullptr) xb[(int64_t)(t0 + t) * H + k] = f32_to_bf16_rne(v);
   }
   __syncthreads();
-  const int rows = (min(T, t0 + kFusedTokens) - t0) * topk;
-  for (int r = tid; r < rows; r += 512) atomicAdd(&cnt[clamp_expert(ids_lds[r], E)], 1);
+  if (active) {
+    float p[kFusedTokens][4];
+#pragma unroll
+    for (int t = 0; t < kFusedTokens; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[t][e] = 0.0f;
+    const float* xl = xs + l;
+    for (int j0 = 0; j0 < nj; j0 += kFusedSteps) {
+      if (j0 > 0) {
+#pragma unroll
+        for (int jj = 0; jj < kFusedSteps; ++jj)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wa[jj][e] = ldg(wl + wo[e] + min(j0 + jj, nj - 1) * kWave);
+      }
+#pragma unroll
+      for (int jj = 0; jj < kFusedSteps; ++jj) {
+        if (j0 + jj < nj) {
+#pragma unroll
+          for (int t = 0; t < kFusedTokens; ++t) {
+            const float xv = xl[min(t, nt - 1) * H + (j0 + jj) * kWave];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[t][e] = __builtin_fmaf(xv, wa[jj][e], p[t][e]);
+          }
+        }
+      }
+    }
+    // lane 16 r of sums[t] holds token t's logit of expert e0 + tree_row_value(r)
+    float flat[kFusedTokens * 4], sums[kFusedTokens];
+#pragma unroll
+    for (int t = 0; t < kFusedTokens; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) flat[t * 4 + e] = p[t][e];
+    tree_sum_quads(flat, sums);
+    const int e = e0 + tree_row_value(l >> 4);
+#pragma unroll
+    for (int t = 0; t < kFusedTokens; ++t) {
+      if ((l & 15) == 0 && t < nt && e < E) {
+        lg[t][e] = sums[t];
+        logits[(int64_t)(t0 + t) * E + e] = sums[t];
+      }
+    }
+  }
+  __syncthreads();
+  if (w < nt) {
+    const int64_t o = (int64_t)(t0 + w) * topk;
+    token_topk(lg[w], E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + w * topk, scratch[w]);
+  }
+  __syncthreads();
+  const int rows = nt * topk;
+  for (int r = tid; r < rows; r += kRouteWaves * kWave) atomicAdd(&cnt[clamp_expert(ids_lds[r], E)], 1);
   __syncthreads();
   if (tid < E) stg(hist + (int64_t)b * E + tid, cnt[tid]);
 }
@@ -621,10 +705,12 @@ __global__ void __launch_bounds__(1024) k_route_small(const float* __restrict__ 
                                                       int renorm, int32_t* ids32, float* wts, GroupTables g) {
   extern __shared__ int lds_group[];
   __shared__ int ids_lds[kSmallTokens * 64];
+  __shared__ uint64_t scratch[16][kTopkScratch];  // blockDim.x <= 1024
   const int nw = (int)(blockDim.x >> 6);
   for (int t = (int)(threadIdx.x >> 6); t < T; t += nw) {
     const int64_t o = (int64_t)t * topk;
-    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + o);
+    token_topk(logits + (int64_t)t * E, E, topk, renorm, ids32 + o, nullptr, wts + o, ids_lds + o,
+               scratch[threadIdx.x >> 6]);
   }
   __syncthreads();
   group_rows([&](int r) { return ids_lds[r]; }, T * topk, E, 1, g, lds_group + 48, lds_group);
@@ -748,10 +834,10 @@ hipError_t launch_logits_topk_group(float* logits, uint16_t* xb, const float* x,
                                     int T, int E, int H, int topk, int renorm, int32_t* ids32, float* wts, int bm,
                                     const GroupTables& g, int32_t* hist, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  if (E > 64 || H % kWave != 0 || topk > 64) return hipErrorInvalidValue;
+  if (E > 64 || H % kWave != 0 || H > kLogitsMaxH || topk > 64) return hipErrorInvalidValue;
   const int blocks = fused_route_blocks(T);
-  UOCR_LAUNCH("logits_topk", k_logits_topk, dim3(blocks), dim3(512), 0, s, logits, xb, x, ldx, router, T, E, H, topk,
-              renorm, ids32, wts, hist);
+  UOCR_LAUNCH("logits_topk", k_logits_topk, dim3(blocks), dim3(kRouteWaves * kWave), 0, s, logits, xb, x, ldx,
+              router, T, E, H, topk, renorm, ids32, wts, hist);
   UOCR_LAUNCH("group_scatter", k_group_scatter_hist, dim3(blocks), dim3(256), 0, s, ids32, T, E, topk, bm, blocks,
               hist, g);
   return hipGetLastError();

@@ -235,7 +235,8 @@ constexpr int kFusedLogitCopyWords = 576;  // 64-bit words per copy (8 tokens x 
 // Task layout, LDS and tagged-buffer sizes of one layer shape.
 struct FusedLayout {
   int gh, gf, gfs;          // 128-element chunks of H, F, Fs
-  int c_gu, c_dn;           // columns per routed gate/up and down task
+  int sub;                  // column blocks per routed task (int8 weights at larger batches: 2)
+  int c_gu, c_dn;           // columns per routed gate/up and down block
   int per_e_gu, per_e_dn;   // routed tasks per selected expert
   int cb_fs, cb_h;          // 64-column blocks of Fs and H
   int n_sgu, n_sdn;         // shared chunk tasks
@@ -246,7 +247,12 @@ struct FusedLayout {
   // offsets (in 64-bit words) of the tagged buffers, sized for 8 tokens
   int64_t off_logits, off_h, off_y, off_hs, off_psgu, off_psdn, data_words;
 };
-FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk);
+// Routed int8 tasks take two column blocks from this many tokens on: a wave
+// then waits for its weights once per two blocks (the int8 stage is half the
+// bf16 one, so two fit the registers).
+constexpr int kFusedSubRows = 4;
+int fused_sub(bool int8, int B);
+FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk, int sub = 1);
 
 struct FusedArgs {
   int B, E, H, F, Fs, topk;
@@ -274,7 +280,7 @@ struct FusedArgs {
   uint64_t* p_sgu;   // [Fs/64][2][H/128][B][64]
   uint64_t* p_sdn;   // [H/64][Fs/128][B][64]
   // layout (FusedLayout)
-  int gh, gf, gfs, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, n_sfold, n_comb, lds_x, lds_act;
+  int gh, gf, gfs, sub, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, n_sfold, n_comb, lds_x, lds_act;
   float inv_gh, inv_gf;
   // polls a wait may take before it fails (sets the error word, takes NaN)
   uint32_t spin_limit;

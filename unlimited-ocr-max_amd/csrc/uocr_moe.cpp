@@ -805,6 +805,7 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.gh = lay.gh;
   a.gf = lay.gf;
   a.gfs = lay.gfs;
+  a.sub = lay.sub;
   a.c_gu = lay.c_gu;
   a.c_dn = lay.c_dn;
   a.per_e_gu = lay.per_e_gu;
@@ -902,7 +903,7 @@ static int decode_rows_impl(const char* op, float* out, const float* x, int64_t 
   const int64_t B = rows, R = rows * L->top_k;
   if (fused_eligible(L, B)) {
     const FusedLayout lay = fused_layout((int)B, (int)L->num_experts, (int)L->hidden, (int)L->ffn,
-                                         (int)L->shared_ffn, (int)L->top_k);
+                                         (int)L->shared_ffn, (int)L->top_k, fused_sub(L->int8 != 0, (int)B));
     FusedSlot slot;
     hipError_t e = hipSuccess;
     if (fixed != nullptr) {
