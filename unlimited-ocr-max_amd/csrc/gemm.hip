@@ -191,12 +191,7 @@ __device__ int xcd_prefix(const GemmProblem& P, const Plan& p, int x) {
     const int c = r - g * p.nr;
     n = row_tiles<BM>(P, g) * min(p.per, p.nt - c * p.per);
   }
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int v = __shfl_up(n, off, kWave);
-    if (q >= off) n += v;
-  }
-  return n;
+  return wave_scan_i(n);
 }
 
 // Tile `it` of XCD x's list (prefix from xcd_prefix).
@@ -876,21 +871,6 @@ struct Units {  // lane v holds the XCD's units v and v + 64 of its problem (hh 
   int n;         // units of the problem (all XCDs)
 };
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-__device__ __forceinline__ int wave_scan_i(int v) {  // inclusive
-  const int l = lane_id();
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int u = __shfl_up(v, off, kWave);
-    if (l >= off) v += u;
-  }
-  return v;
-}
-
 // Problem P's units on XCD x, unit u going to XCD (u0 + u) % 8 (at most 1024
 // units).  Routed: unit u = group u / nt, column u % nt, every row tile.
 // Dense: run u / nt of ceil(row tiles / 8) row tiles, column u % nt.
@@ -903,18 +883,32 @@ __device__ __forceinline__ Units plan_units(const GemmProblem& P, int nt, int ng
   Units q;
   q.n = routed ? ng * nt : (P.M > 0 ? nrun * nt : 0);
   const int xs = ((x - u0) % kXcds + kXcds) % kXcds;
+  // The group tables are read for every lane's unit at once, with the group
+  // clamped to the tables' size, before the group count is known (one memory
+  // latency at the kernel's start instead of two).
+  int gs[2][2], ge[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int u = xs + kXcds * (lane_id() + 64 * hh);
+    gs[hh][0] = gs[hh][1] = ge[hh] = 0;
+    if (routed && P.max_groups > 0) {
+      const int g = min(u / nt, P.max_groups - 1);
+      gs[hh][0] = ldg(P.rows.group_start + g);
+      gs[hh][1] = ldg(P.rows.group_start + g + 1);
+      ge[hh] = ldg(P.rows.group_expert + g);
+    }
+  }
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
     const int u = xs + kXcds * (lane_id() + 64 * hh);
     q.nfull[hh] = q.npart[hh] = q.apart[hh] = q.mt0[hh] = q.c[hh] = q.start[hh] = q.count[hh] = q.e[hh] = 0;
     if (u < q.n) {
-      const int g = routed ? u / nt : 0;
       const int ri = routed ? 0 : u / nt;  // row run (dense)
       int start = 0, count = P.M, e = 0;
       if (routed) {
-        start = ldg(P.rows.group_start + g);
-        count = ldg(P.rows.group_start + g + 1) - start;
-        e = ldg(P.rows.group_expert + g);
+        start = gs[hh][0];
+        count = gs[hh][1] - start;
+        e = ge[hh];
       }
       const int rt = (count + BM - 1) / BM;
       const int mt0 = routed ? 0 : ri * run;
@@ -1076,7 +1070,7 @@ __global__ void __launch_bounds__(kGThreads, kWgPerCu) k_moe_gemm_lds(GemmProble
   };
   // Two rounds at most (small batches): the second round runs in reverse, so
   // that the workgroups with the costliest first tiles take the cheapest
-  // second ones (at T = 512, gate/up 72 -> 62-67 us).  More rounds walk in
+  // second ones (at T = 512, gate/up 70 -> 66 us).  More rounds walk in
   // order (reversing every other round made T = 4096 slower).
   const bool two = sd.total <= 2 * J;
   const int rounds = two ? 2 : (sd.total - j + J - 1) / J;

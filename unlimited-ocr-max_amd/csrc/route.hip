@@ -322,15 +322,6 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-__device__ __forceinline__ int wave_inclusive_sum(int v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int u = __shfl_up(v, d);
-    if (l >= d) v += u;
-  }
-  return v;
-}
 
 // Groups R rows by clamped expert id, stably: a group holds its rows in row
 // order.  `idof(r)` returns row r's raw id.  One workgroup of up to 16 waves
@@ -376,7 +367,7 @@ __device__ void group_rows(IdOf idof, int R, int E, int bm, const GroupTables& g
   }
   const int tiles = c > 0 ? (c + bm - 1) / bm : 0;
   const int nz = c > 0 ? 1 : 0;
-  const int ic = wave_inclusive_sum(c), it = wave_inclusive_sum(tiles), in = wave_inclusive_sum(nz);
+  const int ic = wave_scan_i(c), it = wave_scan_i(tiles), in = wave_scan_i(nz);
   if (lane_id() == kWave - 1) {
     part[w] = ic;
     part[16 + w] = it;
@@ -484,7 +475,7 @@ __global__ void __launch_bounds__(kScatterThreads) k_group_scatter(const int32_t
   const int tot = tid < E ? ldg(total + tid) : 0;
   const int tiles = tot > 0 ? (tot + bm - 1) / bm : 0;
   const int nz = tot > 0 ? 1 : 0;
-  const int ic = wave_inclusive_sum(tot), it = wave_inclusive_sum(tiles), in = wave_inclusive_sum(nz);
+  const int ic = wave_scan_i(tot), it = wave_scan_i(tiles), in = wave_scan_i(nz);
   if (lane_id() == kWave - 1) {
     part[w] = ic;
     part[4 + w] = it;
@@ -671,7 +662,7 @@ __global__ void __launch_bounds__(256) k_group_scatter_hist(const int32_t* __res
     tot = e < E ? part_tot[0][e] + part_tot[1][e] + part_tot[2][e] + part_tot[3][e] : 0;
     const int tiles = tot > 0 ? (tot + bm - 1) / bm : 0;
     const int nz = tot > 0 ? 1 : 0;
-    const int ic = wave_inclusive_sum(tot), it = wave_inclusive_sum(tiles), in = wave_inclusive_sum(nz);
+    const int ic = wave_scan_i(tot), it = wave_scan_i(tiles), in = wave_scan_i(nz);
     const int start = ic - tot, tile0 = it - tiles, grp = in - nz;
     if (e < E) {
       cursor[e] = start + before;

@@ -225,6 +225,37 @@ __device__ __forceinline__ void tree_sum_quads(const float (&v)[N], float (&out)
     out[j] = e;
   }
 }
+// Inclusive prefix sum over the 64 lanes (lane l: v[0] + ... + v[l]) in DPP
+// steps, no LDS round trip: row_shr 1, 2, 4, 8 inside each 16-lane row, then
+// row_bcast 15 (a row's last lane into the next row, rows 1 and 3) and
+// row_bcast 31 (lane 31 into rows 2 and 3).  Integer sums: exact in any order.
+__device__ __forceinline__ int wave_scan_i(int v) {
+  const int l = (int)(threadIdx.x & 63);
+  const int r = l & 15;
+  int t = __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+  if (r >= 1) v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+  if (r >= 2) v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+  if (r >= 4) v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+  if (r >= 8) v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x142, 0xf, 0xf, false);
+  if ((l & 31) >= 16) v += t;
+  t = __builtin_amdgcn_update_dpp(0, v, 0x143, 0xf, 0xf, false);
+  if (l >= 32) v += t;
+  return v;
+}
+// Sum over the 64 lanes, broadcast (the halving tree of tree_sum on integers).
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += (int)from_up<32>((uint32_t)v);
+  v += (int)from_up<16>((uint32_t)v);
+  v += (int)from_up<8>((uint32_t)v);
+  v += (int)from_up<4>((uint32_t)v);
+  v += (int)from_up<2>((uint32_t)v);
+  v += (int)from_up<1>((uint32_t)v);
+  return __builtin_amdgcn_readfirstlane(v);
+}
 __device__ __forceinline__ float tree_max(float v) {
   v = fmaxf(v, from_up<32>(v));
   v = fmaxf(v, from_up<16>(v));
