@@ -179,9 +179,11 @@ def fused_errors() -> int:
 def bench_stack(layers, B: int, steps: int, device: str, seed: int) -> dict:
     """The MoE stack of one decode step: the 11 int8 layers chained through the residual stream,
     x_{l+1} = x_l + MoE_l(x_l) as the decoder's layers add it (so routing differs per layer and the batch's
-    tokens stay distinct), ``steps // 11`` whole steps in one graph.  The step time includes the 11
-    residual adds (one small elementwise kernel each)."""
+    tokens stay distinct), ``steps // 11`` whole steps in one graph.  Two ways, the same bits: one
+    persistent launch for the whole stack (``decode_stack``, the step's figures), and 11 ``decode_rows``
+    launches with their residual adds (one small elementwise kernel each)."""
     import torch
+    from uocr_moe import decode_stack
 
     g = torch.Generator(device=device).manual_seed(seed)
     x0 = rmsnorm_rows(g, B, device)
@@ -191,22 +193,28 @@ def bench_stack(layers, B: int, steps: int, device: str, seed: int) -> dict:
         y, ids, _ = moe.decode_rows(x, workspace=ws, routing=True)
         x = x + y
         u.append(int(torch.unique(ids).numel()))
+    same = bool(torch.equal(decode_stack(layers, x0), x))
 
-    def step():
+    def chained():
         y = x0
         for moe in layers:
             y = y + moe.decode_rows(y, workspace=ws)
 
+    def stacked():
+        decode_stack(layers, x0)
+
     nsteps = max(1, steps // LAYERS)
-    ms = time_graph(graph_of([step] * nsteps))
+    us_c = time_graph(graph_of([chained] * nsteps)) * 1e3 / nsteps
+    us = time_graph(graph_of([stacked] * nsteps)) * 1e3 / nsteps
     errors = fused_errors()
-    us = ms * 1e3 / nsteps
     nbytes = sum(decode_bytes(ui, B, True) for ui in u)
     return {"rows": B, "layers": LAYERS, "us_per_step": round(us, 2), "tokens_per_s": round(B / (us * 1e-6), 1),
             "steps_in_graph": nsteps, "bytes_per_step": nbytes, "hbm_gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "distinct_experts": u,
-            "fused_errors": errors,
-            "chain": "x_{l+1} = x_l + MoE_l(x_l) over the 11 layers (residual adds included), measured"}
+            "fused_errors": errors, "stack_bits_equal_chain": same,
+            "chained_us_per_step": round(us_c, 2), "chained_tokens_per_s": round(B / (us_c * 1e-6), 1),
+            "chain": "x_{l+1} = x_l + MoE_l(x_l) over the 11 layers, measured: one persistent launch "
+                     "(uocr_moe_decode_stack); chained_* = 11 decode_rows launches + 11 residual adds"}
 
 
 def bench_decode(layers, B: int, steps: int, warmup: int, int8: bool, device: str, seed: int) -> dict:
@@ -763,7 +771,8 @@ def main() -> int:
     for B in (1, 8):
         log(f"decode int8, the 11-layer MoE stack chained, B={B}")
         results[f"decode_int8_11layer_step_b{B}"] = bench_stack(layers, B, args.steps, dev, 11 + B)
-        log(f"  {results[f'decode_int8_11layer_step_b{B}']['us_per_step']} us/step")
+        r = results[f"decode_int8_11layer_step_b{B}"]
+        log(f"  {r['us_per_step']} us/step in one launch, {r['chained_us_per_step']} us/step as 11 launches")
     if not args.quick:
         for B in (1, 8):
             log(f"decode step, 12 layers + lm_head, B={B}")

@@ -283,6 +283,25 @@ int uocr_moe_decode_rows_static(float* out, const float* x, int64_t rows, int64_
                                 const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
                                 void* stream, char* err, size_t errlen);
 
+/* uocr_moe_decode_stack -- the MoE blocks of consecutive decoder layers chained
+ * through the residual stream in one persistent launch: x_{l+1} = x_l +
+ * MoE_l(x_l) for l < n_layers, out = x_{n_layers}; each MoE_l is exactly
+ * uocr_moe_decode_rows of layers[l] (the same bits), and the adds are the
+ * residual adds of unlimited_ocr_max/decoder.py:709 (`x + self.mlp.decode_rows(...)`)
+ * with nothing between them.  No single call of the reference matches it: it
+ * serves the MoE stack of a decode step (the 11 MoE layers of
+ * decoder.py:790-791 with their attention taken out), where one launch replaces
+ * n_layers launches and n_layers adds.  rows <= 8; 1 <= n_layers <= 12 layers
+ * of one shape and kind, each of which uocr_moe_decode_rows would run on the
+ * persistent kernel (other layers are refused: chain uocr_moe_decode_rows for
+ * them).  Each stream that makes such calls holds a zeroed arena of tagged
+ * words (about 100 MB) until uocr_moe_release(); a call outside stream capture
+ * makes the first and keeps one spare for a stream first seen under capture, so
+ * a stacked call is made outside capture before one is captured. */
+int uocr_moe_decode_stack(float* out, const float* x, int64_t rows, int64_t hidden,
+                          const uocr_moe_layer* const* layers, int64_t n_layers, void* stream, char* err,
+                          size_t errlen);
+
 /* MoE.__call__ (prefill) -- replaces unlimited_ocr_max/decoder.py:657-667
  * (the dense 64-expert chain of the int8 path, _routed_native of the bf16
  * path).  x fp32 [T, H] -> out fp32 [T, H].  The top-k experts of every token

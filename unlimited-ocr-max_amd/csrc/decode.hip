@@ -326,10 +326,11 @@ __device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) {
 // tables (same steps as route.hip's k_softmax_topk: max, exp, halving-tree
 // sum, divide; the k largest probabilities in turn, ties to the lower id),
 // then one more on the workgroup's count of routed tokens.
-__device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int t, uint32_t tag, int* r_ids,
+__device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int64_t boff, int t, uint32_t tag,
+                                                           int* r_ids,
                                                            float* r_wts, int* r_done, uint64_t* keys) {
   const int l = lane();
-  const uint64_t* src = A.logits + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
+  const uint64_t* src = A.logits + boff + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + (l < A.E ? l : A.E - 1);
   uint64_t q;
   uint32_t spin = A.spin_limit;
   const bool wtrace = kTrace && A.trace != nullptr && t == 0 && l == 0;
@@ -421,8 +422,8 @@ __device__ __forceinline__ i32x4 ld16(const void* p) { return *(const UOCR_GLOBA
 // (int8) or 256 (bf16) contiguous bytes; lanes past the task repeat its last
 // lane's row.
 template <bool INT8>
-__device__ __attribute__((always_inline)) void issue_routed(const KA FusedArgs& A, bool gu, int e, int n0, int ncols,
-                                                            Stage<INT8>& st) {
+__device__ __attribute__((always_inline)) void issue_routed(const KA FusedArgs& A, const KA FusedLayerW& W, bool gu,
+                                                            int e, int n0, int ncols, Stage<INT8>& st) {
   const int l = lane();
   const int G = gu ? A.gh : A.gf;
   const int N = gu ? A.F : A.H;
@@ -431,7 +432,7 @@ __device__ __attribute__((always_inline)) void issue_routed(const KA FusedArgs& 
   const int cp = small_div(lam, gu ? A.inv_gh : A.inv_gf);
   const int g = lam - cp * G;
   const int c = gu ? cp >> 1 : cp;
-  const char* w = (const char*)(gu ? ((cp & 1) ? A.up_w : A.gate_w) : A.down_w);
+  const char* w = (const char*)(gu ? ((cp & 1) ? W.up_w : W.gate_w) : W.down_w);
   const char* p = w + (((int64_t)e * N + n0 + c) * (gu ? A.H : A.F) + (int64_t)g * 128) * esz;
 #pragma unroll
   for (int i = 0; i < (INT8 ? 8 : 16); ++i) st.v[i] = ld16(p + 16 * i);
@@ -526,6 +527,9 @@ struct Ctx {
   float* act;       // the wave's activation stage
   uint32_t tag;
   int t;            // the running task (tracing)
+  int layer;        // the layer of a stack (0 for one layer)
+  int64_t boff;     // the layer's tagged buffers, in words from the first layer's
+  const KA FusedLayerW* W;  // the layer's weights
 };
 
 // Router task of expert e: the lane's router weights (k = l + 64 j), loaded
@@ -534,9 +538,10 @@ struct Ctx {
 constexpr int kMaxJ = 32;  // H <= 2048
 constexpr int kRouterWaves = kFusedRouterWaves;  // router tasks per workgroup
 
-__device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A, int e, float (&w)[kMaxJ]) {
+__device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A, const KA FusedLayerW& W, int e,
+                                                           float (&w)[kMaxJ]) {
   const int l = lane();
-  const float* wr = A.router + (int64_t)e * A.H + l;
+  const float* wr = W.router + (int64_t)e * A.H + l;
   const int nk = A.H / kWave;
 #pragma unroll
   for (int j = 0; j < kMaxJ; ++j) w[j] = ldg(wr + (j < nk ? j : nk - 1) * kWave);
@@ -556,7 +561,7 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
     for (int j = 0; j < kMaxJ; ++j)
       if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
     const float v = tree_sum(p);
-    if (l == 0) st_pair_xcd(A.logits + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + e, v, C.tag);
+    if (l == 0) st_pair_xcd(A.logits + C.boff + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + e, v, C.tag);
   }
   if (t0 == 0) UOCR_TRACE(A, C.t, 4);
 }
@@ -564,7 +569,7 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
 // Shared gate or up, 64 columns x chunk g of H, every token: partials.
 __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, const Ctx& C, const Task& k,
                                                         Stage<false>& st) {
-  uint64_t* dst = A.p_sgu + ((int64_t)(k.a * 2 + k.b) * A.gh + k.c) * A.B * 64 + lane();
+  uint64_t* dst = A.p_sgu + C.boff + ((int64_t)(k.a * 2 + k.b) * A.gh + k.c) * A.B * 64 + lane();
   for (int r = 0; r < A.B; ++r) {
     launder(st);
     st_pair(dst + r * 64, chain<false>(st, C.xs + (r * A.gh + k.c) * kXPad), C.tag);
@@ -573,7 +578,7 @@ __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, c
 
 __device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   Stage<false> st;
-  issue_kblocked(k.b ? A.sh_up : A.sh_gate, A.Fs, k.a * 64, k.c, st);
+  issue_kblocked(k.b ? C.W->sh_up : C.W->sh_gate, A.Fs, k.a * 64, k.c, st);
   UOCR_TRACE_LOADS(A, C.t);
   sgu_rows(A, C, k, st);
 }
@@ -588,7 +593,8 @@ __device__ __attribute__((always_inline)) void task_sfold(const KA FusedArgs& A,
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     float v[kMaxG];
-    poll_pairs<kMaxG>(A.p_sgu + ((int64_t)(k.a * 2 + p) * A.gh * A.B + r) * 64 + l, (int64_t)A.B * 64, A.gh, C.tag,
+    poll_pairs<kMaxG>(A.p_sgu + C.boff + ((int64_t)(k.a * 2 + p) * A.gh * A.B + r) * 64 + l, (int64_t)A.B * 64, A.gh,
+                      C.tag,
                       A.ctl, A.spin_limit, v);
     float sum = 0.0f;
 #pragma unroll
@@ -597,7 +603,7 @@ __device__ __attribute__((always_inline)) void task_sfold(const KA FusedArgs& A,
     acc[p] = sum;
   }
   UOCR_TRACE(A, C.t, 3);
-  st_pair(A.hs + (int64_t)r * A.Fs + k.a * 64 + l, silu(acc[0]) * acc[1], C.tag);
+  st_pair(A.hs + C.boff + (int64_t)r * A.Fs + k.a * 64 + l, silu(acc[0]) * acc[1], C.tag);
 }
 
 // Shared down, 64 columns x chunk g of Fs, every token: partials.
@@ -605,14 +611,14 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   const int l = lane();
   const int g = k.b;
   Stage<false> st;
-  issue_kblocked(A.sh_down, A.H, k.a * 64, g, st);
+  issue_kblocked(C.W->sh_down, A.H, k.a * 64, g, st);
   UOCR_TRACE_LOADS(A, C.t);
   // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
   {
     // pair i is row i/2, element (i%2)*64 + l; the first pair is probed first
     constexpr int kMaxP = 16;
     const int np = 2 * A.B;
-    const uint64_t* src = A.hs + (int64_t)g * 128 + l;
+    const uint64_t* src = A.hs + C.boff + (int64_t)g * 128 + l;
     float v[kMaxP];
     uint32_t spin = A.spin_limit;
     while (!poll_done(pair_has(ld_pair(src), C.tag), spin, A.ctl)) {
@@ -644,7 +650,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
     __builtin_amdgcn_wave_barrier();
   }
   UOCR_TRACE(A, C.t, 3);
-  uint64_t* dst = A.p_sdn + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
+  uint64_t* dst = A.p_sdn + C.boff + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
   for (int r = 0; r < A.B; ++r) {
     launder(st);
     st_pair(dst + r * 64, chain<false>(st, C.act + r * 128), C.tag);
@@ -659,6 +665,9 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
 template <bool INT8, int MAXG>
 __device__ __forceinline__ float fold_groups(float part, float scale, int base, int G) {
   constexpr int kBatch = 8;  // shuffles in flight (registers)
+  // G through an empty asm: the group bounds below are compared where they
+  // are used, not hoisted out of the enclosing loops as live masks
+  asm volatile("" : "+s"(G));
   float acc = 0.0f;
 #pragma unroll
   for (int g0 = 0; g0 < MAXG; g0 += kBatch) {
@@ -713,11 +722,11 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
     bk.ncols[j] = min(A.c_gu, A.F - bk.n0[j]);
     bk.scale[j] = 0.0f;
     if (bk.ncols[j] > 0) {
-      issue_routed<INT8>(A, true, e, bk.n0[j], bk.ncols[j], bk.st[j]);
+      issue_routed<INT8>(A, *C.W, true, e, bk.n0[j], bk.ncols[j], bk.st[j]);
       if constexpr (INT8) {
         const int lam = min(l, 2 * bk.ncols[j] * A.gh - 1);
         const int cp = small_div(lam, A.inv_gh);
-        bk.scale[j] = ldg(((cp & 1) ? A.up_s : A.gate_s) + ((int64_t)e * A.F + bk.n0[j] + (cp >> 1)) * A.gh +
+        bk.scale[j] = ldg(((cp & 1) ? C.W->up_s : C.W->gate_s) + ((int64_t)e * A.F + bk.n0[j] + (cp >> 1)) * A.gh +
                           (lam - cp * A.gh));
       }
     }
@@ -743,7 +752,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
       const float acc = fold_groups<INT8, kMaxG>(part, bk.scale[j], base, A.gh);
       UOCR_TRACE(A, C.t, 4);
       const float up = shfl(acc, min(l + A.gh, kWave - 1));
-      if (writer) st_pair(A.h + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
+      if (writer) st_pair(A.h + C.boff + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
     }
   }
 }
@@ -767,11 +776,11 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
     bk.ncols[j] = min(A.c_dn, A.H - bk.n0[j]);
     bk.scale[j] = 0.0f;
     if (bk.ncols[j] > 0) {
-      issue_routed<INT8>(A, false, e, bk.n0[j], bk.ncols[j], bk.st[j]);
+      issue_routed<INT8>(A, *C.W, false, e, bk.n0[j], bk.ncols[j], bk.st[j]);
       if constexpr (INT8) {
         const int lam = min(l, bk.ncols[j] * A.gf - 1);
         const int c = small_div(lam, A.inv_gf);
-        bk.scale[j] = ldg(A.down_s + ((int64_t)e * A.H + bk.n0[j] + c) * A.gf + (lam - c * A.gf));
+        bk.scale[j] = ldg(C.W->down_s + ((int64_t)e * A.H + bk.n0[j] + c) * A.gf + (lam - c * A.gf));
       }
     }
   }
@@ -780,7 +789,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   while (rows != 0ull) {
     const int r = (int)__builtin_ctzll(rows);
     rows &= rows - 1ull;
-    const uint64_t* src = A.h + (int64_t)r * A.F + l;
+    const uint64_t* src = A.h + C.boff + (int64_t)r * A.F + l;
     for (int i0 = 0; i0 < npairs; i0 += kMaxP) {
       float v[kMaxP];
       // The probe is the row's last pair (its columns come from the expert's
@@ -813,7 +822,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
       const float part = chain<INT8>(bk.st[j], C.act + g * kXPad);
       const float acc = fold_groups<INT8, kMaxG>(part, bk.scale[j], c * A.gf, A.gf);
       UOCR_TRACE(A, C.t, 4);
-      if (g == 0 && l < lanes) st_pair(A.y + (int64_t)r * A.H + bk.n0[j] + c, acc, C.tag);
+      if (g == 0 && l < lanes) st_pair(A.y + C.boff + (int64_t)r * A.H + bk.n0[j] + c, acc, C.tag);
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -830,13 +839,15 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   // a failed earlier launch leaves the error word set: every output is then NaN until the host clears it
   const uint32_t failed = ld_word(A.ctl + C_ERR);
   float v[kMaxG];
-  poll_pairs<kMaxG>(A.p_sdn + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag, A.ctl, A.spin_limit, v);
+  poll_pairs<kMaxG>(A.p_sdn + C.boff + ((int64_t)k.a * A.gfs * A.B + t) * 64 + l, (int64_t)A.B * 64, A.gfs, C.tag,
+                    A.ctl, A.spin_limit, v);
   float shv = 0.0f;
 #pragma unroll
   for (int g = 0; g < kMaxG; ++g)
     if (g < A.gfs) shv = shv + v[g];
   float y[kMaxK];
-  poll_pairs<kMaxK, kPollFull>(A.y + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl, A.spin_limit, y);
+  poll_pairs<kMaxK, kPollFull>(A.y + C.boff + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl,
+                               A.spin_limit, y);
   UOCR_TRACE(A, C.t, 3);
   float wj[kMaxK];
 #pragma unroll
@@ -845,7 +856,17 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j)
     if (j < A.topk) acc = __builtin_fmaf(wj[j], y[j], acc);
-  A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : acc + shv;
+  const float res = acc + shv;
+  if (!A.residual) {
+    A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : res;
+  } else {
+    // the residual stream: x_{l+1} = x_l + MoE_l(x_l), x_l from the LDS rows
+    const float xn = C.xs[t * A.gh * kXPad + (n >> 7) * kXPad + (n & 127)] + res;
+    if (C.layer + 1 < A.n_layers)
+      st_pair(A.xs_pairs + ((int64_t)C.layer * A.B + t) * A.H + n, failed != 0u ? __builtin_nanf("") : xn, C.tag);
+    else
+      A.out[(int64_t)t * A.H + n] = failed != 0u ? __builtin_nanf("") : xn;
+  }
 }
 
 // Runs task t (INT8: the routed experts' weights are int8 with scales).
@@ -911,102 +932,162 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   const bool router = wave < kRouterWaves && re < n_router;
   const int r_e = re % A.E;
   const int r_t0 = (re / A.E) * A.r_tok;
-  int t = A.E + rank;
-
-  // a router task's weights do not depend on x: they load while x is staged
-  float w[kMaxJ];
-  if (router) router_load(A, r_e, w);
-
-  // x rows into LDS, each 128-element chunk padded to kXPad floats: 16-byte
-  // pieces (a chunk is 32 of them), every thread's loads issued before the
-  // first is used, in little code (each launch runs it with cold caches)
-  if (A.x_vec) {
-    constexpr int kXPasses = (8 * 2048 / 4 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
-    const int n4 = A.B * A.H / 4;
-    f32x4 xv[kXPasses];
-#pragma unroll
-    for (int j = 0; j < kXPasses; ++j) {
-      const int i = (int)threadIdx.x + j * kThreads;
-      if (i < n4) xv[j] = *(const UOCR_GLOBAL f32x4*)(A.x + 4 * i);
-    }
-#pragma unroll
-    for (int j = 0; j < kXPasses; ++j) {
-      const int i = (int)threadIdx.x + j * kThreads;
-      if (i < n4) {
-        const int r = (4 * i) / A.H;
-        const int kk = 4 * i - r * A.H;
-        *(f32x4*)(xs + r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)) = xv[j];
-      }
-    }
-  } else {
-    for (int i = (int)threadIdx.x; i < A.B * A.H; i += kThreads) {
-      const int r = i / A.H;
-      const int kk = i - r * A.H;
-      xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
-    }
-  }
-  // One load of the epoch per workgroup (3 072 waves loading the one word at
-  // once would queue every workgroup's start behind it), shared through LDS.
-  // The last wave does it (and the arrival count below): its first work is
-  // to wait for the logits, while the router tasks run on the first waves.
   constexpr int kCtlThread = kThreads - kWave;
   uint32_t* lds_epoch = (uint32_t*)(lds + A.lds_x + 516);
-  if (threadIdx.x == kCtlThread) {
-    *r_done = 0;
-    *lds_epoch = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
-    if (kTrace && A.trace != nullptr) {
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-      A.trace[A.trace_wg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
-    }
-  }
-  __syncthreads();
-  const uint32_t epoch = __builtin_amdgcn_readfirstlane(*lds_epoch);
-  C.tag = epoch + 1u;
-  // the arrival count; its returned value is read after the control wave's tasks
-  uint32_t arrived = 0u;
-  if (threadIdx.x == kCtlThread)
-    arrived = __hip_atomic_fetch_add(A.ctl + C_ARRIVED + (blockIdx.x % kSpread) * kLine, 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t arrived = 0u, epoch = 0u;
 
-  if (router) {
-    // the trace keeps one record per expert: XCD 0's task of its first tokens
-    const bool traced = r_t0 == 0 && blockIdx.x % kXcds == 0;
-    C.t = r_e;
-    if (traced) UOCR_TRACE(A, r_e, 0);
-    if (traced) UOCR_TRACE_LOADS(A, r_e);
-    router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
-    if (traced) UOCR_TRACE(A, r_e, 2);
-    if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
-  }
-  // The routing of token i is computed by wave kWaves-1-i (high waves, whose
-  // tasks come late in the list); the other waves meanwhile run their tasks
-  // that do not need the routing (the shared experts).
-  const int rwave = kWaves - 1 - wave;
-  // (the routing wave's activation stage, idle until its first task, holds the keys)
-  if (rwave < A.B) route_token(A, rwave, C.tag, r_ids, r_wts, r_done, (uint64_t*)C.act);
-  // One task loop (one copy of the task code): the first routed task waits
-  // for the workgroup's routing.
-  Route rt{0ull, 0, r_ids, 0};
-  int n_tasks = unrouted_count(A);
-  bool routed = false;
-  int64_t troute = 0;
-  for (;; t += nwaves) {
-    if (!routed && t >= n_tasks) {
+  // One layer, or a stack of layers chained through the residual stream: a
+  // workgroup starts layer l + 1 once every one of its waves is done with
+  // layer l (its LDS tables are then free) and the layer's input, x_{l+1} as
+  // tagged pairs from every combine task of layer l, has arrived.  Each layer
+  // has buffers of its own, so no wait of layer l can see layer l + 1's data.
+  for (int layer = 0; layer < Ap->n_layers; ++layer) {
+    // the arguments through an opaque pointer each layer: nothing derived
+    // from them is hoisted out of the loop, where it would stay live (and
+    // spill) across every layer
+    const KA FusedArgs* Al = Ap;
+    asm volatile("" : "+s"(Al));
+    const KA FusedArgs& A = *Al;
+    // the thread index the same way, for the x staging's per-pass indices
+    int tid = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    C.layer = layer;
+    C.boff = (int64_t)layer * A.layer_words;
+    C.W = &A.w[layer];
+    int t = A.E + rank;
+
+    // a router task's weights do not depend on x: they load while x is staged
+    // (defined for every wave, so that no value is carried from the previous layer)
+    float w[kMaxJ];
+#pragma unroll
+    for (int j = 0; j < kMaxJ; ++j) w[j] = 0.0f;
+    if (router) router_load(A, *C.W, r_e, w);
+    if (layer > 0) __syncthreads();  // every wave is done with the previous layer
+
+    // x rows into LDS, each 128-element chunk padded to kXPad floats
+    if (layer > 0) {
+      // x_l as tagged pairs: every thread's pairs loaded and their values
+      // written to the LDS rows, until all of the wave's carry the tag
+      constexpr int kPPasses = (8 * 2048 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
+      const int n = A.B * A.H;
+      const uint64_t* src = A.xs_pairs + (int64_t)(layer - 1) * n;
       uint32_t spin = A.spin_limit;
-      while (!poll_done(__hip_atomic_load(r_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= A.B, spin,
-                        A.ctl)) {
+      for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < kPPasses; ++j) {
+          const int i = tid + j * kThreads;
+          if (i < n) {
+            const uint64_t q = ld_pair(src + i);
+            const int r = i / A.H;
+            const int kk = i - r * A.H;
+            xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = pair_value(q);
+            ok = ok && pair_has(q, C.tag);
+          }
+        }
+        if (poll_done(ok, spin, A.ctl)) break;
       }
-      asm volatile("" ::: "memory");
-      if (kTrace && A.trace != nullptr) troute = (int64_t)wall_clock64();
-      // without the routing (a failed wait), no routed task runs: the combine's waits for them fail too
-      rt = expired(spin) ? Route{0ull, 0, r_ids, 0} : make_route(A, r_ids);
-      n_tasks = task_count(A, rt.ng);
-      routed = true;
+      if (expired(spin)) {
+        for (int i = tid; i < n; i += kThreads) {
+          const int r = i / A.H;
+          const int kk = i - r * A.H;
+          xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = __builtin_nanf("");
+        }
+      }
+    } else if (A.x_vec) {
+      // 16-byte pieces (a chunk is 32 of them), every thread's loads issued
+      // before the first is used, in little code (each launch runs it with
+      // cold caches)
+      constexpr int kXPasses = (8 * 2048 / 4 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
+      const int n4 = A.B * A.H / 4;
+      f32x4 xv[kXPasses];
+#pragma unroll
+      for (int j = 0; j < kXPasses; ++j) {
+        const int i = tid + j * kThreads;
+        xv[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // (no value carried from another layer)
+        if (i < n4) xv[j] = *(const UOCR_GLOBAL f32x4*)(A.x + 4 * i);
+      }
+#pragma unroll
+      for (int j = 0; j < kXPasses; ++j) {
+        const int i = tid + j * kThreads;
+        if (i < n4) {
+          const int r = (4 * i) / A.H;
+          const int kk = 4 * i - r * A.H;
+          *(f32x4*)(xs + r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)) = xv[j];
+        }
+      }
+    } else {
+      for (int i = tid; i < A.B * A.H; i += kThreads) {
+        const int r = i / A.H;
+        const int kk = i - r * A.H;
+        xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
+      }
     }
-    if (t >= n_tasks) break;
-    const KA FusedArgs* Ai = Ap;
-    asm volatile("" : "+s"(Ai));
-    run_task<INT8>(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
+    // One load of the epoch per workgroup and launch (3 072 waves loading the
+    // one word at once would queue every workgroup's start behind it), shared
+    // through LDS.  The last wave does it (and the arrival count below): its
+    // first work is to wait for the logits, while the router tasks run on the
+    // first waves.
+    if (threadIdx.x == kCtlThread) {
+      *r_done = 0;
+      if (layer == 0) {
+        *lds_epoch = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
+        if (kTrace && A.trace != nullptr) {
+          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+          A.trace[A.trace_wg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
+        }
+      }
+    }
+    __syncthreads();
+    if (layer == 0) {
+      epoch = __builtin_amdgcn_readfirstlane(*lds_epoch);
+      C.tag = epoch + 1u;
+      // the arrival count; its returned value is read after the control wave's tasks
+      if (threadIdx.x == kCtlThread)
+        arrived = __hip_atomic_fetch_add(A.ctl + C_ARRIVED + (blockIdx.x % kSpread) * kLine, 1u, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    if (router) {
+      // the trace keeps one record per expert: XCD 0's task of its first tokens
+      const bool traced = r_t0 == 0 && blockIdx.x % kXcds == 0;
+      C.t = r_e;
+      if (traced) UOCR_TRACE(A, r_e, 0);
+      if (traced) UOCR_TRACE_LOADS(A, r_e);
+      router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
+      if (traced) UOCR_TRACE(A, r_e, 2);
+      if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
+    }
+    // The routing of token i is computed by wave kWaves-1-i (high waves, whose
+    // tasks come late in the list); the other waves meanwhile run their tasks
+    // that do not need the routing (the shared experts).
+    const int rwave = kWaves - 1 - wave;
+    // (the routing wave's activation stage, idle until its first task, holds the keys)
+    if (rwave < A.B) route_token(A, C.boff, rwave, C.tag, r_ids, r_wts, r_done, (uint64_t*)C.act);
+    // One task loop (one copy of the task code): the first routed task waits
+    // for the workgroup's routing.
+    Route rt{0ull, 0, r_ids, 0};
+    int n_tasks = unrouted_count(A);
+    bool routed = false;
+    int64_t troute = 0;
+    for (;; t += nwaves) {
+      if (!routed && t >= n_tasks) {
+        uint32_t spin = A.spin_limit;
+        while (!poll_done(__hip_atomic_load(r_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= A.B, spin,
+                          A.ctl)) {
+        }
+        asm volatile("" ::: "memory");
+        if (kTrace && A.trace != nullptr) troute = (int64_t)wall_clock64();
+        // without the routing (a failed wait), no routed task runs: the combine's waits for them fail too
+        rt = expired(spin) ? Route{0ull, 0, r_ids, 0} : make_route(A, r_ids);
+        n_tasks = task_count(A, rt.ng);
+        routed = true;
+      }
+      if (t >= n_tasks) break;
+      const KA FusedArgs* Ai = Ap;
+      asm volatile("" : "+s"(Ai));
+      run_task<INT8>(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
+    }
   }
   // Two-level arrival count: the workgroup that completes its counter (of the
   // workgroups b with the same b % kSpread) adds to C_ARRIVED2, and the one that

@@ -254,9 +254,8 @@ constexpr int kFusedSubRows = 4;
 int fused_sub(bool int8, int B);
 FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk, int sub = 1);
 
-struct FusedArgs {
-  int B, E, H, F, Fs, topk;
-  int int8, renorm;
+// One layer's weights (the stacked layouts of uocr_moe_layer).
+struct FusedLayerW {
   const float* router;
   const void* gate_w;
   const void* up_w;
@@ -267,6 +266,21 @@ struct FusedArgs {
   const uint16_t* sh_gate;
   const uint16_t* sh_up;
   const uint16_t* sh_down;
+};
+constexpr int kFusedMaxLayers = 12;  // layers of one stacked launch
+
+struct FusedArgs {
+  int B, E, H, F, Fs, topk;
+  int int8, renorm;
+  // residual = 0: one layer, out = MoE(x) (n_layers = 1).  residual = 1: a
+  // stack of n_layers chained through the residual stream, x_{l+1} = x_l +
+  // MoE_l(x_l), out = x_n; layer l's tagged buffers at l * layer_words from
+  // those below, x_{l+1} (l < n - 1) as tagged pairs [B][H] at xs_pairs + l * B * H.
+  int residual;
+  int n_layers;
+  int64_t layer_words;
+  uint64_t* xs_pairs;
+  FusedLayerW w[kFusedMaxLayers];
   const float* x;
   float* out;
   int32_t* ids_out;  // optional routing outputs [B*topk]

@@ -140,6 +140,8 @@ struct FusedDevice {
   std::vector<void*> chunks;
   std::vector<FusedSlot> spare;
   std::map<hipStream_t, FusedSlot> slot;
+  std::map<hipStream_t, uint64_t*> stack;  // tagged arenas of stacked launches (fused_stack_words)
+  std::vector<uint64_t*> stack_spare;      // one kept for a stream first seen under capture
   hipStream_t last_stream = nullptr;  // stream of the last eager persistent launch
   hipEvent_t handoff = nullptr;       // orders eager launches on different streams
 };
@@ -211,6 +213,61 @@ hipError_t fused_slot(hipStream_t stream, FusedSlot* out, bool* need_alloc) {
   d.slot[stream] = *out;
   // keep a spare for a stream that first appears under capture
   if (d.spare.empty() && !cap) e = fused_grow(d, stream);
+  return e;
+}
+
+// Tagged words of a stacked launch's arena: kFusedMaxLayers layers of the
+// largest eligible layer's buffers, then the residual stream x_{l+1} of every
+// layer but the last as tagged pairs [8][2048].
+int64_t fused_stack_words() { return (int64_t)kFusedMaxLayers * (fused_max_words() + 8 * 2048); }
+
+// A new zeroed stacked-launch arena (g_ws_mu held, not under capture).
+hipError_t fused_stack_grow(FusedDevice& d, hipStream_t stream) {
+  const size_t bytes = (size_t)fused_stack_words() * 8;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return e;
+  e = launch_zero_words(static_cast<uint32_t*>(p), (int64_t)(bytes / 4), stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);  // zero before any stream uses it
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return e;
+  }
+  d.chunks.push_back(p);  // freed with the slots
+  d.stack_spare.push_back(static_cast<uint64_t*>(p));
+  return hipSuccess;
+}
+
+// The stacked-launch arena of (current device, stream), as fused_slot hands
+// out slots: a stream seen for the first time takes the spare arena (made by
+// an earlier call outside capture) or, outside capture, a new one; a spare is
+// then made again outside capture.  *need_alloc is set when a stream first
+// seen under capture finds no spare.  Kept until uocr_moe_release().
+hipError_t fused_stack_arena(hipStream_t stream, uint64_t** out, bool* need_alloc) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  FusedDevice& d = g_fused[dev];
+  *need_alloc = false;
+  auto it = d.stack.find(stream);
+  if (it != d.stack.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  const bool cap = capturing(stream);
+  if (d.stack_spare.empty()) {
+    if (cap) {
+      *need_alloc = true;
+      return hipSuccess;
+    }
+    e = fused_stack_grow(d, stream);
+    if (e != hipSuccess) return e;
+  }
+  *out = d.stack_spare.back();
+  d.stack_spare.pop_back();
+  d.stack[stream] = *out;
+  if (d.stack_spare.empty() && !cap) e = fused_stack_grow(d, stream);
   return e;
 }
 
@@ -775,6 +832,21 @@ static uint32_t fused_spin_limit() {
   return 1u << 16;
 }
 
+static FusedLayerW fused_weights(const uocr_moe_layer* L) {
+  FusedLayerW w;
+  w.router = L->router;
+  w.gate_w = L->gate_proj;
+  w.up_w = L->up_proj;
+  w.down_w = L->down_proj;
+  w.gate_s = L->gate_proj_scales;
+  w.up_s = L->up_proj_scales;
+  w.down_s = L->down_proj_scales;
+  w.sh_gate = L->shared_gate;
+  w.sh_up = L->shared_up;
+  w.sh_down = L->shared_down;
+  return w;
+}
+
 static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayout& lay, const FusedSlot& f) {
   FusedArgs a{};
   a.B = (int)B;
@@ -785,16 +857,8 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.topk = (int)L->top_k;
   a.int8 = L->int8;
   a.renorm = L->renormalize;
-  a.router = L->router;
-  a.gate_w = L->gate_proj;
-  a.up_w = L->up_proj;
-  a.down_w = L->down_proj;
-  a.gate_s = L->gate_proj_scales;
-  a.up_s = L->up_proj_scales;
-  a.down_s = L->down_proj_scales;
-  a.sh_gate = L->shared_gate;
-  a.sh_up = L->shared_up;
-  a.sh_down = L->shared_down;
+  a.n_layers = 1;
+  a.w[0] = fused_weights(L);
   a.ctl = f.ctl;
   a.logits = f.data + lay.off_logits;
   a.h = f.data + lay.off_h;
@@ -1105,6 +1169,66 @@ int uocr_moe_decode_rows_static(float* out, const float* x, int64_t rows, int64_
   const FusedSlot fixed{reinterpret_cast<uint32_t*>(base), reinterpret_cast<uint64_t*>(base + (size_t)kFusedCtlWords * 4)};
   return decode_rows_impl(op, out, x, rows, hidden, L, expert_ids, expert_weights, base + kScratchFusedBytes,
                           kScratchBytes - kScratchFusedBytes, s, &fixed, err, errlen);
+}
+
+int uocr_moe_decode_stack(float* out, const float* x, int64_t rows, int64_t hidden,
+                          const uocr_moe_layer* const* layers, int64_t n_layers, void* stream, char* err,
+                          size_t errlen) {
+  const char* op = "uocr_moe_decode_stack";
+  if (layers == nullptr || n_layers < 1 || n_layers > kFusedMaxLayers)
+    return fail(err, errlen, "%s: n_layers must be in [1, %d]", op, kFusedMaxLayers);
+  const uocr_moe_layer* L0 = layers[0];
+  for (int64_t l = 0; l < n_layers; ++l) {
+    const uocr_moe_layer* L = layers[l];
+    if (check_layer(op, L, hidden, err, errlen)) return 1;
+    if (L->num_experts != L0->num_experts || L->hidden != L0->hidden || L->ffn != L0->ffn ||
+        L->shared_ffn != L0->shared_ffn || L->top_k != L0->top_k || L->int8 != L0->int8 ||
+        L->group != L0->group || L->renormalize != L0->renormalize)
+      return fail(err, errlen, "%s: layer %lld differs in shape or kind from layer 0", op, (long long)l);
+  }
+  if (rows < 0 || rows > 8) return fail(err, errlen, "%s: rows must be in [0, 8]", op);
+  if (rows == 0) return 0;
+  for (int64_t l = 0; l < n_layers; ++l)
+    if (!fused_eligible(layers[l], rows))
+      return fail(err, errlen, "%s: layer %lld does not take the persistent decode kernel (shapes, alignment or "
+                  "UOCR_MOE_DECODE=multi); chain uocr_moe_decode_rows instead", op, (long long)l);
+  const int64_t B = rows;
+  const hipStream_t s = (hipStream_t)stream;
+  const FusedLayout lay = fused_layout((int)B, (int)L0->num_experts, (int)L0->hidden, (int)L0->ffn,
+                                       (int)L0->shared_ffn, (int)L0->top_k, fused_sub(L0->int8 != 0, (int)B));
+  FusedSlot slot;
+  bool need_alloc = false;
+  hipError_t e = fused_slot(s, &slot, &need_alloc);
+  uint64_t* arena = nullptr;
+  if (e == hipSuccess && !need_alloc) e = fused_stack_arena(s, &arena, &need_alloc);
+  if (e == hipSuccess && need_alloc)
+    return fail(err, errlen, "%s: no arena for a new stream under capture (make a stacked call on this stream "
+                "outside stream capture first)", op);
+  if (e == hipSuccess) e = fused_order(s);
+  int grid = 0;
+  if (e == hipSuccess) e = fused_grid_cached(lay.lds_bytes, &grid);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+  if (grid < 1) return fail(err, errlen, "%s: the persistent decode kernel does not fit a CU", op);
+  // the layers' buffers in the stack arena, the control words in the stream's slot
+  FusedArgs a = fused_args(L0, B, lay, FusedSlot{slot.ctl, arena});
+  a.residual = 1;
+  a.n_layers = (int)n_layers;
+  a.layer_words = fused_max_words();
+  a.xs_pairs = arena + (int64_t)kFusedMaxLayers * fused_max_words();
+  for (int64_t l = 0; l < n_layers; ++l) a.w[l] = fused_weights(layers[l]);
+  const int64_t router_slots = (int64_t)(grid / kFusedXcds) * kFusedRouterWaves;
+  a.r_tok = 1;
+  while (a.r_tok < B && L0->num_experts * ((B + a.r_tok - 1) / a.r_tok) > router_slots) ++a.r_tok;
+  if (grid % kFusedXcds != 0 || L0->num_experts * ((B + a.r_tok - 1) / a.r_tok) > router_slots)
+    return fail(err, errlen, "%s: the persistent decode kernel needs a grid of whole XCDs with room for its "
+                "router tasks", op);
+  a.x = x;
+  a.x_vec = aligned16(x) ? 1 : 0;
+  a.out = out;
+  a.ids_out = nullptr;
+  a.wts_out = nullptr;
+  e = launch_decode_fused(a, grid, lay.lds_bytes, s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
 
 int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, const uocr_moe_layer* L,

@@ -65,6 +65,7 @@ SIGNATURES: dict[str, list] = {
     "uocr_moe_gate": [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _int, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_decode_rows": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_decode_rows_static": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _cp, _sz],
+    "uocr_moe_decode_stack": [_vp, _vp, _i64, _i64, ctypes.POINTER(ctypes.POINTER(Layer)), _i64, _vp, _cp, _sz],
     "uocr_moe_forward": [_vp, _vp, _i64, _i64, ctypes.POINTER(Layer), _vp, _vp, _vp, _sz, _vp, _cp, _sz],
     "uocr_moe_release": [],
     "uocr_moe_timing_begin": [_int, _cp, _sz],

@@ -139,6 +139,21 @@ class MoE:
         return gate(x, self.router, self.config.num_experts_per_tok, renormalize=self.config.renormalize)
 
 
+def decode_stack(layers: "list[MoE]", x: torch.Tensor) -> torch.Tensor:
+    """The MoE blocks of consecutive decoder layers on the residual stream, one launch:
+    ``x_{l+1} = x_l + layers[l].decode_rows(x_l)`` (the adds of decoder.py:709 with the attention
+    taken out), returning ``x_n``; the same bits as chaining ``decode_rows``.  Up to 12 layers of
+    one shape and kind, ``x [B, H]`` with B <= 8."""
+    op = "uocr_moe_decode_stack"
+    x = _gpu(op, "x", x, torch.float32, 2)
+    if not layers:
+        raise ValueError(f"{op}: no layers")
+    out = torch.empty_like(x)
+    ptrs = (ctypes.POINTER(_lib.Layer) * len(layers))(*[ctypes.pointer(m._layer) for m in layers])
+    _lib.call(op, out.data_ptr(), x.data_ptr(), int(x.shape[0]), int(x.shape[1]), ptrs, len(layers), _stream(x))
+    return out
+
+
 def gate(x: torch.Tensor, router: torch.Tensor, top_k: int, *, renormalize: bool = False):
     """Softmax over the experts, then top-k in score order, ties to the lower id."""
     op = "uocr_moe_gate"
