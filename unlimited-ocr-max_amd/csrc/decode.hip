@@ -662,12 +662,13 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
 // lane as partial_g), or the plain sum (bf16).  Every shuffle of a batch is
 // issued before its first add (a shuffle under the loop's bound would wait for
 // each one in turn).
-template <bool INT8, int MAXG>
+template <bool INT8, int MAXG, bool STACK>
 __device__ __forceinline__ float fold_groups(float part, float scale, int base, int G) {
   constexpr int kBatch = 8;  // shuffles in flight (registers)
-  // G through an empty asm: the group bounds below are compared where they
-  // are used, not hoisted out of the enclosing loops as live masks
-  asm volatile("" : "+s"(G));
+  // In the stacked kernel, G through an empty asm: the group bounds below are
+  // compared where they are used, not hoisted out of the layer loop as masks
+  // live (and spilled) across every layer
+  if constexpr (STACK) asm volatile("" : "+s"(G));
   float acc = 0.0f;
 #pragma unroll
   for (int g0 = 0; g0 < MAXG; g0 += kBatch) {
@@ -708,7 +709,7 @@ struct Blocks {
 // H, the expert's routed rows: h = silu(fold(gate)) * fold(up), fold over the
 // 128-groups in order.  Lane l of a block is (column, projection, group) =
 // ((2c + p) * gh + g).
-template <bool INT8, int SUB>
+template <bool INT8, int SUB, bool STACK>
 __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
@@ -749,7 +750,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
       rows &= rows - 1ull;
       launder(bk.st[j]);
       const float part = chain<INT8>(bk.st[j], C.xs + ((r / A.topk) * A.gh + g) * kXPad);
-      const float acc = fold_groups<INT8, kMaxG>(part, bk.scale[j], base, A.gh);
+      const float acc = fold_groups<INT8, kMaxG, STACK>(part, bk.scale[j], base, A.gh);
       UOCR_TRACE(A, C.t, 4);
       const float up = shfl(acc, min(l + A.gh, kWave - 1));
       if (writer) st_pair(A.h + C.boff + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
@@ -761,7 +762,7 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
 // row by row: y = fold over the 128-groups in order.  Lane l of a block is
 // (column, group of F) = (c * gf + g).  A row of h is polled once for all
 // blocks.
-template <bool INT8, int SUB>
+template <bool INT8, int SUB, bool STACK>
 __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, const Ctx& C, const Route& rt,
                                                         const Task& k) {
   constexpr int kMaxG = 16;
@@ -820,7 +821,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
       const int g = lam - c * A.gf;
       launder(bk.st[j]);
       const float part = chain<INT8>(bk.st[j], C.act + g * kXPad);
-      const float acc = fold_groups<INT8, kMaxG>(part, bk.scale[j], c * A.gf, A.gf);
+      const float acc = fold_groups<INT8, kMaxG, STACK>(part, bk.scale[j], c * A.gf, A.gf);
       UOCR_TRACE(A, C.t, 4);
       if (g == 0 && l < lanes) st_pair(A.y + C.boff + (int64_t)r * A.H + bk.n0[j] + c, acc, C.tag);
     }
@@ -869,8 +870,9 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   }
 }
 
-// Runs task t (INT8: the routed experts' weights are int8 with scales).
-template <bool INT8>
+// Runs task t (INT8: the routed experts' weights are int8 with scales;
+// STACK: in the stacked kernel).
+template <bool INT8, bool STACK>
 __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, const Ctx& C0, const Route& rt, int t,
                                                         const Task& k, int64_t troute) {
   Ctx C = C0;
@@ -884,13 +886,13 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
     case K_SGU: task_sgu(A, C, k); break;
     case K_RGU:
       if (INT8 && A.sub == 2)
-        task_rgu<INT8, 2>(A, C, rt, k);
+        task_rgu<INT8, 2, STACK>(A, C, rt, k);
       else
-        task_rgu<INT8, 1>(A, C, rt, k);
+        task_rgu<INT8, 1, STACK>(A, C, rt, k);
       break;
     case K_SFOLD: task_sfold(A, C, k); break;
     case K_SDN: task_sdn(A, C, k); break;
-    case K_RDN: task_rdn<INT8, 1>(A, C, rt, k); break;
+    case K_RDN: task_rdn<INT8, 1, STACK>(A, C, rt, k); break;
     case K_COMB: task_comb(A, C, k); break;
     default: break;
   }
@@ -900,8 +902,9 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
 }
 
 // One instantiation per routed weight type, each with its own register
-// allocation (the bf16 stage is twice the int8 one).
-template <bool INT8>
+// allocation (the bf16 stage is twice the int8 one), and per kind of launch:
+// one layer (STACK = false, no layer loop), or a stack of layers.
+template <bool INT8, bool STACK>
 __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   (void)args;  // read in place, through the kernel-argument segment
   const KA FusedArgs* Ap = (const KA FusedArgs*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -941,16 +944,18 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   // layer l (its LDS tables are then free) and the layer's input, x_{l+1} as
   // tagged pairs from every combine task of layer l, has arrived.  Each layer
   // has buffers of its own, so no wait of layer l can see layer l + 1's data.
-  for (int layer = 0; layer < Ap->n_layers; ++layer) {
-    // the arguments through an opaque pointer each layer: nothing derived
-    // from them is hoisted out of the loop, where it would stay live (and
-    // spill) across every layer
+  const int n_layers = STACK ? Ap->n_layers : 1;
+  for (int layer = 0; layer < n_layers; ++layer) {
+    // In the stacked kernel the arguments and the thread index pass through
+    // empty asms each layer: nothing derived from them is hoisted out of the
+    // loop, where it would stay live (and spill) across every layer.
     const KA FusedArgs* Al = Ap;
-    asm volatile("" : "+s"(Al));
-    const KA FusedArgs& A = *Al;
-    // the thread index the same way, for the x staging's per-pass indices
     int tid = (int)threadIdx.x;
-    asm volatile("" : "+v"(tid));
+    if constexpr (STACK) {
+      asm volatile("" : "+s"(Al));
+      asm volatile("" : "+v"(tid));
+    }
+    const KA FusedArgs& A = *Al;
     C.layer = layer;
     C.boff = (int64_t)layer * A.layer_words;
     C.W = &A.w[layer];
@@ -959,13 +964,15 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     // a router task's weights do not depend on x: they load while x is staged
     // (defined for every wave, so that no value is carried from the previous layer)
     float w[kMaxJ];
+    if constexpr (STACK) {
 #pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) w[j] = 0.0f;
+      for (int j = 0; j < kMaxJ; ++j) w[j] = 0.0f;
+    }
     if (router) router_load(A, *C.W, r_e, w);
-    if (layer > 0) __syncthreads();  // every wave is done with the previous layer
+    if (STACK && layer > 0) __syncthreads();  // every wave is done with the previous layer
 
     // x rows into LDS, each 128-element chunk padded to kXPad floats
-    if (layer > 0) {
+    if (STACK && layer > 0) {
       // x_l as tagged pairs: every thread's pairs loaded and their values
       // written to the LDS rows, until all of the wave's carry the tag
       constexpr int kPPasses = (8 * 2048 + kThreads - 1) / kThreads;  // B <= 8, H <= 2048
@@ -1004,7 +1011,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
 #pragma unroll
       for (int j = 0; j < kXPasses; ++j) {
         const int i = tid + j * kThreads;
-        xv[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // (no value carried from another layer)
+        if constexpr (STACK) xv[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};  // (no value carried from another layer)
         if (i < n4) xv[j] = *(const UOCR_GLOBAL f32x4*)(A.x + 4 * i);
       }
 #pragma unroll
@@ -1086,7 +1093,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
       if (t >= n_tasks) break;
       const KA FusedArgs* Ai = Ap;
       asm volatile("" : "+s"(Ai));
-      run_task<INT8>(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
+      run_task<INT8, STACK>(*Ai, C, rt, t, task_at(*Ai, rt.ng, t), troute);
     }
   }
   // Two-level arrival count: the workgroup that completes its counter (of the
@@ -1156,19 +1163,23 @@ FusedLayout fused_layout(int B, int E, int H, int F, int Fs, int topk, int sub) 
 
 bool fused_trace_built() { return kTrace; }
 
-// The resident capacity of both instantiations (the smaller, so that one
-// grid suits either).
+// The resident capacity of every instantiation (the smallest, so that one
+// grid suits any).
 hipError_t fused_grid(size_t lds_bytes, int* grid) {
-  int dev = 0, cus = 0, per_cu[2] = {0, 0};
+  int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const void* kernels[2] = {(const void*)k_decode_fused<true>, (const void*)k_decode_fused<false>};
-  for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+  const void* kernels[4] = {(const void*)k_decode_fused<true, false>, (const void*)k_decode_fused<false, false>,
+                            (const void*)k_decode_fused<true, true>, (const void*)k_decode_fused<false, true>};
+  int per_cu[4] = {0, 0, 0, 0};
+  for (int i = 0; i < 4 && e == hipSuccess; ++i) {
     e = hipFuncSetAttribute(kernels[i], hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu[i], kernels[i], kThreads, lds_bytes);
   }
   if (e != hipSuccess) return e;
-  *grid = cus * (per_cu[0] < per_cu[1] ? per_cu[0] : per_cu[1]);
+  int least = per_cu[0];
+  for (int i = 1; i < 4; ++i) least = per_cu[i] < least ? per_cu[i] : least;
+  *grid = cus * least;
   return hipSuccess;
 }
 
@@ -1177,10 +1188,17 @@ hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, h
   if (grid % kXcds != 0 || a.r_tok < 1 ||
       (int64_t)(grid / kXcds) * kRouterWaves < (int64_t)a.E * ((a.B + a.r_tok - 1) / a.r_tok))
     return hipErrorInvalidConfiguration;
-  if (a.int8)
-    UOCR_LAUNCH("decode_fused", k_decode_fused<true>, dim3(grid), dim3(kThreads), lds_bytes, s, a);
-  else
-    UOCR_LAUNCH("decode_fused", k_decode_fused<false>, dim3(grid), dim3(kThreads), lds_bytes, s, a);
+  if (a.residual) {
+    if (a.int8)
+      UOCR_LAUNCH("decode_stack", (k_decode_fused<true, true>), dim3(grid), dim3(kThreads), lds_bytes, s, a);
+    else
+      UOCR_LAUNCH("decode_stack", (k_decode_fused<false, true>), dim3(grid), dim3(kThreads), lds_bytes, s, a);
+  } else {
+    if (a.int8)
+      UOCR_LAUNCH("decode_fused", (k_decode_fused<true, false>), dim3(grid), dim3(kThreads), lds_bytes, s, a);
+    else
+      UOCR_LAUNCH("decode_fused", (k_decode_fused<false, false>), dim3(grid), dim3(kThreads), lds_bytes, s, a);
+  }
   return hipGetLastError();
 }
 
