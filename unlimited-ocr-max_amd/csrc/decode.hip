@@ -552,8 +552,9 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
                                                            const float (&w)[kMaxJ]) {
   const int l = lane();
   const int nk = A.H / kWave;
-  for (int t = t0; t < t1; ++t) {
-    const float* xr = C.xs + t * A.gh * kXPad + l;
+  uint64_t* dst = A.logits + C.boff + (blockIdx.x % kXcds) * kLogitCopyWords + e;
+  if (t1 - t0 == 1) {
+    const float* xr = C.xs + t0 * A.gh * kXPad + l;
     // (issuing every read before the chain made the layer slower at one
     // token, though the chain itself got shorter)
     float p = 0.0f;
@@ -561,7 +562,29 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
     for (int j = 0; j < kMaxJ; ++j)
       if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
     const float v = tree_sum(p);
-    if (l == 0) st_pair_xcd(A.logits + C.boff + (blockIdx.x % kXcds) * kLogitCopyWords + t * 64 + e, v, C.tag);
+    if (l == 0) st_pair_xcd(dst + t0 * 64, v, C.tag);
+  } else {
+    // four tokens' chains side by side (each in its own order), their lane
+    // sums in one quad tree: lane 16 r holds token t + tree_row_value(r)'s
+    for (int t = t0; t < t1; t += 4) {
+      const float* xr[4];
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xr[i] = C.xs + min(t + i, t1 - 1) * A.gh * kXPad + l;
+        p[i] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kMaxJ; ++j)
+        if (j < nk) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[i] = __builtin_fmaf(xr[i][(j >> 1) * kXPad + kWave * (j & 1)], w[j], p[i]);
+        }
+      float v[1];
+      tree_sum_quads<4>(p, v);
+      const int tt = t + tree_row_value(l >> 4);
+      if ((l & 15) == 0 && tt < t1) st_pair_xcd(dst + tt * 64, v[0], C.tag);
+    }
   }
   if (t0 == 0) UOCR_TRACE(A, C.t, 4);
 }
