@@ -134,6 +134,31 @@ def test_decode_full_int8_bitwise(oracle, full_int8, B, decode_path) -> None:
         assert bits_equal(got, single)
 
 
+def test_decode_routing_ties(oracle, full_int8, decode_path) -> None:
+    """Equal router logits on the decode path: token 0 has two pairs of tied experts (3 = 9 and
+    20 = 40, identical router rows) on top, token 1 is all zeros (all 64 logits tie: experts 0-5),
+    token 2 has none; ids, weights and outputs bitwise the oracle's (ties to the lower id)."""
+    import dataclasses
+
+    x = oracle.rmsnorm_rows(np.random.default_rng(31), 3, 1280)
+    x[0, 0] = 10.0
+    x[1, :] = 0.0
+    router = full_int8.router.copy()
+    router[:, 0] = 0.0
+    router[[3, 20], 0] = 1.0
+    router[9] = router[3]
+    router[40] = router[20]
+    tied = dataclasses.replace(full_int8, router=np.ascontiguousarray(router))
+    moe = moe_for(tied)
+    for B in (1, 3):
+        out, ids, wts = moe.decode_rows(t(x[:B]), routing=True)
+        want, ids_o, wts_o = oracle.moe_decode_exact(x[:B], tied)
+        assert np.array_equal(n(ids), ids_o) and bits_equal(n(wts), wts_o)
+        assert bits_equal(n(out), want)
+    assert ids_o[0, :4].tolist() == [3, 9, 20, 40]
+    assert ids_o[1].tolist() == [0, 1, 2, 3, 4, 5]
+
+
 @pytest.mark.parametrize("B", [1, 2, 8])
 def test_decode_full_bf16_bitwise(oracle, full_bf16, B, decode_path) -> None:
     moe = moe_for(full_bf16)

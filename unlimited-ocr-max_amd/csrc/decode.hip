@@ -255,41 +255,47 @@ __device__ __forceinline__ int task_count(const KA FusedArgs& A, int ng) {
 // for the sgu partials, follow the routed gate/up tasks.
 __device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.E + A.n_sgu; }
 
+// x / d from m = ceil(2^32 / d) (0 for d = 1), exact while x * d < 2^32: a
+// multiply-high in place of an integer division's ~40 dependent instructions,
+// in the task list's decoding and the stacked kernel's x polls (11-layer
+// step B=1 202 -> 191 us, B=8 595 -> 568 us; the single layer's x staging
+// kept its division, which measured faster there).
+__device__ __forceinline__ int task_div(int x, uint32_t m) { return m ? (int)__umulhi((uint32_t)x, m) : x; }
+
 // Task order: router, sgu, rgu, sfold, sdn, rdn, comb (every task waits only
 // for tasks before it).
 __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
   if (t < A.E) return {K_ROUTER, t, 0, 0};
   t -= A.E;
   if (t < A.n_sgu) {
-    const int per_u = 2 * A.gh;
-    const int u = t / per_u;
-    const int r = t - u * per_u;
-    const int p = r / A.gh;
+    const int u = task_div(t, A.m_2gh);
+    const int r = t - u * 2 * A.gh;
+    const int p = task_div(r, A.m_gh);
     return {K_SGU, u, p, r - p * A.gh};
   }
   t -= A.n_sgu;
   if (t < ng * A.per_e_gu) {
-    const int s = t / A.per_e_gu;
+    const int s = task_div(t, A.m_gu);
     return {K_RGU, s, t - s * A.per_e_gu, 0};
   }
   t -= ng * A.per_e_gu;
   if (t < A.n_sfold) {
-    const int u = t / A.B;
+    const int u = task_div(t, A.m_b);
     return {K_SFOLD, u, t - u * A.B, 0};
   }
   t -= A.n_sfold;
   if (t < A.n_sdn) {
-    const int cb = t / A.gfs;
+    const int cb = task_div(t, A.m_gfs);
     return {K_SDN, cb, t - cb * A.gfs, 0};
   }
   t -= A.n_sdn;
   if (t < ng * A.per_e_dn) {
-    const int s = t / A.per_e_dn;
+    const int s = task_div(t, A.m_dn);
     return {K_RDN, s, t - s * A.per_e_dn, 0};
   }
   t -= ng * A.per_e_dn;
   if (t < A.n_comb) {
-    const int cb = t / A.B;
+    const int cb = task_div(t, A.m_b);
     return {K_COMB, cb, t - cb * A.B, 0};
   }
   return {K_NONE, 0, 0, 0};
@@ -354,11 +360,17 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   // compares, where selecting in turn is six dependent wave reductions).
   const uint64_t key = real ? ((((uint64_t)__float_as_uint(pr)) << 6) | (uint64_t)(63 - l)) + 1ull : 0ull;
   keys[l] = key;
+  // (each half's 16 reads issued before its compares: left to the scheduler,
+  // the reads went out one or two at a time, each waited for in turn)
   int rank = 0;
 #pragma unroll
-  for (int j = 0; j < kWave; j += 2) {
-    const u64x2 kk = *(const u64x2*)(keys + j);
-    rank += (kk[0] > key ? 1 : 0) + (kk[1] > key ? 1 : 0);
+  for (int h = 0; h < kWave; h += 32) {
+    u64x2 kk[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) kk[j] = *(const u64x2*)(keys + h + 2 * j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) rank += (kk[j][0] > key ? 1 : 0) + (kk[j][1] > key ? 1 : 0);
   }
   const bool chosen = real && rank < A.topk;
   float my_w = pr;
@@ -1009,7 +1021,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
           const int i = tid + j * kThreads;
           if (i < n) {
             const uint64_t q = ld_pair(src + i);
-            const int r = i / A.H;
+            const int r = task_div(i, A.m_h);
             const int kk = i - r * A.H;
             xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = pair_value(q);
             ok = ok && pair_has(q, C.tag);
@@ -1019,7 +1031,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
       }
       if (expired(spin)) {
         for (int i = tid; i < n; i += kThreads) {
-          const int r = i / A.H;
+          const int r = task_div(i, A.m_h);
           const int kk = i - r * A.H;
           xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = __builtin_nanf("");
         }
@@ -1048,7 +1060,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
       }
     } else {
       for (int i = tid; i < A.B * A.H; i += kThreads) {
-        const int r = i / A.H;
+        const int r = task_div(i, A.m_h);
         const int kk = i - r * A.H;
         xs[r * A.gh * kXPad + (kk >> 7) * kXPad + (kk & 127)] = ldg(A.x + i);
       }

@@ -296,6 +296,10 @@ struct FusedArgs {
   // layout (FusedLayout)
   int gh, gf, gfs, sub, c_gu, c_dn, per_e_gu, per_e_dn, cb_fs, cb_h, n_sgu, n_sdn, n_sfold, n_comb, lds_x, lds_act;
   float inv_gh, inv_gf;
+  // the kernel's divisors d as m = ceil(2^32 / d) (0 for d = 1): x / d =
+  // mulhi(x, m) exactly while x * d < 2^32 (task indices stay below 2^20,
+  // element indices below 2^14, divisors below 2^12)
+  uint32_t m_2gh, m_gh, m_gu, m_b, m_gfs, m_dn, m_h;
   // polls a wait may take before it fails (sets the error word, takes NaN)
   uint32_t spin_limit;
   int r_tok;  // tokens per router task

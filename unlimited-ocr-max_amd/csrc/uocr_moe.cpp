@@ -884,6 +884,14 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.lds_act = lay.lds_act;
   a.inv_gh = 1.0f / (float)lay.gh;
   a.inv_gf = 1.0f / (float)lay.gf;
+  auto magic = [](int d) { return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d); };
+  a.m_2gh = magic(2 * lay.gh);
+  a.m_gh = magic(lay.gh);
+  a.m_gu = magic(lay.per_e_gu);
+  a.m_b = magic(B);
+  a.m_gfs = magic(lay.gfs);
+  a.m_dn = magic(lay.per_e_dn);
+  a.m_h = magic(a.H);
   a.spin_limit = fused_spin_limit();
   return a;
 }

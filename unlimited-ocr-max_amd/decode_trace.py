@@ -94,6 +94,8 @@ def trace(B: int) -> None:
     w = wg[wg[:, 0] > 0]
     print(f"| workgroup steps | {len(w)} | entry {q(us(w[:, 6]))} | epoch read {q(us(w[:, 7]))} | "
           f"logits seen {q(us(w[:, 1]))} | top-k {q(us(w[:, 5]))} | routing published {q(us(w[:, 2]))} |")
+    print(f"| routing steps (token 0) | {len(w)} | logits seen {q(us(w[:, 1]))} | max {q(us(w[:, 3]))} | "
+          f"exp sum {q(us(w[:, 4]))} | ranks {q(us(w[:, 5]))} | published {q(us(w[:, 2]))} |")
 
 
 if __name__ == "__main__":
