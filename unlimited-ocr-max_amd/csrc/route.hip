@@ -571,12 +571,40 @@ __global__ void __launch_bounds__(kRouteWaves * 64) k_logits_topk(
 #pragma unroll
       for (int e = 0; e < 4; ++e) wa[jj][e] = ldg(wl + wo[e] + min(jj, nj - 1) * kWave);
   }
-  for (int i = tid; i < nt * H; i += kRouteWaves * kWave) {
-    const int t = i / H;
-    const int k = i - t * H;
-    const float v = ldg(x + (int64_t)(t0 + t) * ldx + k);
-    xs[t * H + k] = v;
-    if (xb != nullptr) xb[(int64_t)(t0 + t) * H + k] = f32_to_bf16_rne(v);
+  if ((((uintptr_t)x | (uintptr_t)(ldx * 4) | (uintptr_t)(H * 4)) & 15) == 0) {
+    // 16-byte pieces, every thread's loads issued before the first is stored
+    // (a loop of single loads waited out one memory latency per element)
+    constexpr int kXv = kFusedTokens * kLogitsMaxH / 4 / (kRouteWaves * kWave);
+    const int h4 = H / 4;
+    f32x4 xv[kXv];
+#pragma unroll
+    for (int j = 0; j < kXv; ++j) {
+      const int i = tid + j * kRouteWaves * kWave;
+      const int t = min(i / h4, nt - 1);
+      xv[j] = *(const f32x4*)(x + (int64_t)(t0 + t) * ldx + 4 * (i - (i / h4) * h4));
+    }
+#pragma unroll
+    for (int j = 0; j < kXv; ++j) {
+      const int i = tid + j * kRouteWaves * kWave;
+      const int t = i / h4;
+      const int k = 4 * (i - t * h4);
+      if (t < nt) {
+        *(f32x4*)(xs + t * H + k) = xv[j];
+        if (xb != nullptr) {
+          const uint32_t lo = (uint32_t)f32_to_bf16_rne(xv[j].x) | ((uint32_t)f32_to_bf16_rne(xv[j].y) << 16);
+          const uint32_t hi = (uint32_t)f32_to_bf16_rne(xv[j].z) | ((uint32_t)f32_to_bf16_rne(xv[j].w) << 16);
+          *(uint2*)(xb + (int64_t)(t0 + t) * H + k) = make_uint2(lo, hi);
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < nt * H; i += kRouteWaves * kWave) {
+      const int t = i / H;
+      const int k = i - t * H;
+      const float v = ldg(x + (int64_t)(t0 + t) * ldx + k);
+      xs[t * H + k] = v;
+      if (xb != nullptr) xb[(int64_t)(t0 + t) * H + k] = f32_to_bf16_rne(v);
+    }
   }
   __syncthreads();
   if (active) {
