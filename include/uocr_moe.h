@@ -320,11 +320,22 @@ void uocr_moe_release(void);
  * on the device's static scratch) ran out of its bounded waits: errors = 1.
  * Such a launch wrote NaN where its outputs depended on what it waited for,
  * and every later launch on the same slot writes NaN until this call, which
- * then clears the slot (control words and tagged arena).  The waits run out
- * only when the persistent kernel's workgroups cannot all be resident, i.e.
- * another kernel holds CUs for tens of milliseconds.  No counterpart in the
- * reference; the error path of this build's decode kernel. */
+ * then clears the slot's error word (the launch epoch keeps counting, so no
+ * value the failed launch left behind can satisfy a later launch's waits).
+ * The waits run out only when the persistent kernel's workgroups cannot all
+ * be resident, i.e. another kernel holds CUs for tens of milliseconds.  No
+ * counterpart in the reference; the error path of this build's decode kernel. */
 int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errlen);
+
+/* The same report without a synchronisation: enqueues on `stream` one tiny
+ * kernel that writes flag[0] (device memory, one uint32) = 1 if the error word
+ * of `stream`'s slot or of the device's static scratch is set, else 0.  Stream
+ * ordered after the decode launches before it, so a serving loop reads the
+ * flag with its outputs (or tests it on the device); capturable in a graph.
+ * It clears nothing: after a 1, uocr_moe_fused_errors resets the slot.  No
+ * counterpart in the reference (its ops fail on the host only,
+ * kernels/moe_int8.mojo:194-210); the error path of this build's decode kernel. */
+int uocr_moe_fused_status(uint32_t* flag, void* stream, char* err, size_t errlen);
 
 /* Arms a phase trace for the next persistent decode launch: for task i it
  * writes 8 int64 words at buffer[8i] (device memory, `words` long):

@@ -71,7 +71,7 @@ def full_bf16(oracle):
 def test_prefill_t512_zipf(oracle, full_int8, full_bf16, which) -> None:
     x, layer = _zipf_layer(oracle, full_int8 if which == "int8" else full_bf16, 512, 512)
     hist = _prefill_check(oracle, layer, x, f"prefill {which} T=512 Zipf")
-    assert hist.max() > 100 and (hist == 0).sum() >= 1, hist
+    assert hist.max() > 100 and (hist == 0).sum() >= 4, hist  # the skew the workload asks for: idle experts
 
 
 def test_prefill_t4096_zipf(oracle, full_int8) -> None:

@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 import torch
 
-from _gpu import bits_equal, differ, moe_for, n, t
+from _gpu import DEV, bits_equal, differ, moe_for, n, t
 
 pytestmark = pytest.mark.gpu
 
@@ -388,15 +388,20 @@ def test_decode_failure_is_loud_and_recoverable(oracle, small, monkeypatch) -> N
     moe = moe_for(layer)
     x = np.random.default_rng(31).standard_normal((4, 256)).astype(np.float32)
     want = oracle.moe_decode_exact(x, layer)[0]
-    assert bits_equal(n(moe.decode_rows(t(x))), want)
+    flag = torch.full((1,), 7, dtype=torch.int32, device=DEV)
+    assert bits_equal(n(moe.decode_rows(t(x), status=flag)), want)
+    assert int(flag.item()) == 0
     assert _lib.fused_errors() == 0
     monkeypatch.setenv("UOCR_MOE_SPIN_LIMIT", "0")
-    failed = n(moe.decode_rows(t(x)))
+    failed = n(moe.decode_rows(t(x), status=flag))
     monkeypatch.delenv("UOCR_MOE_SPIN_LIMIT")
     assert np.isnan(failed).all()
-    assert np.isnan(n(moe.decode_rows(t(x)))).all()  # the slot stays poisoned
+    assert int(flag.item()) == 1  # seen in the caller's buffer, stream-ordered, no fused_errors call
+    assert np.isnan(n(moe.decode_rows(t(x), status=flag))).all()  # the slot stays poisoned
+    assert int(flag.item()) == 1
     assert _lib.fused_errors() == 1  # reported, and cleared
-    assert bits_equal(n(moe.decode_rows(t(x))), want)
+    assert bits_equal(n(moe.decode_rows(t(x), status=flag)), want)
+    assert int(flag.item()) == 0
     assert _lib.fused_errors() == 0
 
 

@@ -61,6 +61,35 @@ def test_stack_eleven_full_int8_layers(B) -> None:
     assert _lib.fused_errors() == 0
 
 
+def test_stack_recovers_after_a_failed_launch(oracle, monkeypatch) -> None:
+    """A stacked launch whose bounded waits are forced to fail from the host (a spin limit of 0; every
+    kernel still ends normally) reports through the stream-ordered status flag and ``fused_errors``;
+    after the reset, more stacked launches than ran before the failure (their launch tags climbing past
+    every tag the failed and earlier launches left in the arenas) are each bitwise the chained calls."""
+    from uocr_moe import _lib, decode_stack
+
+    moes = [moe_for(oracle.make_layer(60 + i, E=64, H=256, F=128, int8=True, std=0.05, router_std=0.1))
+            for i in range(3)]
+    xs = [t(oracle.rmsnorm_rows(np.random.default_rng(600 + i), 1 + i % 4, 256)) for i in range(4)]
+    wants = [n(_chain(moes, x)) for x in xs]
+    flag = torch.full((1,), 7, dtype=torch.int32, device=DEV)
+    k = 3
+    for i in range(k):
+        assert bits_equal(n(decode_stack(moes, xs[i % 4], status=flag)), wants[i % 4])
+        assert int(flag.item()) == 0
+    monkeypatch.setenv("UOCR_MOE_SPIN_LIMIT", "0")
+    failed = n(decode_stack(moes, xs[0], status=flag))
+    monkeypatch.delenv("UOCR_MOE_SPIN_LIMIT")
+    assert np.isnan(failed).all()
+    assert int(flag.item()) == 1
+    assert _lib.fused_errors() == 1
+    for i in range(2 * k + 2):
+        got = n(decode_stack(moes, xs[i % 4], status=flag))
+        assert bits_equal(got, wants[i % 4]), (i, differ(got, wants[i % 4]))
+        assert int(flag.item()) == 0
+    assert _lib.fused_errors() == 0
+
+
 def test_stack_refusals(oracle) -> None:
     from uocr_moe import UocrError, decode_stack
 

@@ -197,3 +197,8 @@ def test_static_decode_refuses_beyond_its_scratch() -> None:
     assert msg.startswith("uocr_moe_decode_rows_static: 64 rows of this layer need ") and "more than the" in msg
     msg = _err("uocr_moe_decode_rows_static", None, None, 65, 2048, ctypes.byref(layer), None, None, None)
     assert msg == "uocr_moe_decode_rows_static: rows must be in [0, 64]"
+
+
+def test_fused_status_refuses_a_missing_flag() -> None:
+    """The stream-ordered error flag entry refuses a null flag before any device call."""
+    assert _err("uocr_moe_fused_status", None, None) == "uocr_moe_fused_status: no flag"

@@ -79,3 +79,33 @@ def test_static_entry_refuses_beyond_its_scratch(oracle, layers) -> None:
     with pytest.raises(UocrError, match="rows must be in"):
         _lib.call("uocr_moe_decode_rows_static", x.data_ptr(), x.data_ptr(), 65, 1280, ctypes.byref(moe._layer),
                   None, None, _stream(x))
+
+
+def test_static_entry_refuses_a_workspace_beyond_its_scratch(oracle, layers) -> None:
+    """A layer the persistent kernel does not take (64 rows, top-8 of 8 experts, widths 2048) needs more than
+    the 7 MiB multi-kernel part of the static scratch: refused with the size before anything is enqueued;
+    the next static call is still bitwise decode_rows."""
+    from uocr_moe import UocrError, _lib
+    from uocr_moe.ops import _stream
+
+    E, H, F, Fs, k, G = 8, 2048, 2048, 4096, 8, 128
+    dev = DEV
+    # every buffer the layer names exists at full size (never read: the call is refused first)
+    w = {name: torch.empty(shape, dtype=dt, device=dev) for name, shape, dt in (
+        ("router", (E, H), torch.float32), ("gate", (E, F, H), torch.int8), ("up", (E, F, H), torch.int8),
+        ("down", (E, H, F), torch.int8), ("gs", (E, F, H // G), torch.float32), ("us", (E, F, H // G), torch.float32),
+        ("ds", (E, H, F // G), torch.float32), ("sg", (Fs, H), torch.bfloat16), ("su", (Fs, H), torch.bfloat16),
+        ("sd", (H, Fs), torch.bfloat16))}
+    L = _lib.Layer(num_experts=E, hidden=H, ffn=F, shared_ffn=Fs, top_k=k, group=G, int8=1, renormalize=0,
+                   router=w["router"].data_ptr(), gate_proj=w["gate"].data_ptr(), up_proj=w["up"].data_ptr(),
+                   down_proj=w["down"].data_ptr(), gate_proj_scales=w["gs"].data_ptr(),
+                   up_proj_scales=w["us"].data_ptr(), down_proj_scales=w["ds"].data_ptr(),
+                   shared_gate=w["sg"].data_ptr(), shared_up=w["su"].data_ptr(), shared_down=w["sd"].data_ptr())
+    x = torch.zeros((64, H), device=dev)
+    out = torch.zeros_like(x)
+    with pytest.raises(UocrError, match="need [0-9]+ bytes of scratch"):
+        _lib.call("uocr_moe_decode_rows_static", out.data_ptr(), x.data_ptr(), 64, H, ctypes.byref(L), None, None,
+                  _stream(x))
+    moe = moe_for(layers["small"])
+    xs = t(oracle.rmsnorm_rows(np.random.default_rng(91), 5, 256))
+    assert bits_equal(n(_static(moe, xs)), n(moe.decode_rows(xs)))

@@ -1253,4 +1253,19 @@ hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t s) {
   return hipGetLastError();
 }
 
+// flag[0] = the OR of the error words at a and b (either may be null), read
+// with the agent-scope loads the persistent kernel writes them with.
+__global__ void k_error_status(uint32_t* flag, const uint32_t* a, const uint32_t* b) {
+  if (threadIdx.x != 0) return;
+  uint32_t v = 0u;
+  if (a != nullptr) v |= ld_word(a + C_ERR);
+  if (b != nullptr) v |= ld_word(b + C_ERR);
+  flag[0] = v != 0u ? 1u : 0u;
+}
+
+hipError_t launch_error_status(uint32_t* flag, const uint32_t* ctl_a, const uint32_t* ctl_b, hipStream_t s) {
+  UOCR_LAUNCH("error_status", k_error_status, dim3(1), dim3(64), 0, s, flag, ctl_a, ctl_b);
+  return hipGetLastError();
+}
+
 }  // namespace uocr

@@ -411,26 +411,75 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
+// v[0..3] of the 4 lanes of a quad (qd = lane & 3) as a 4 x 4 matrix, lane
+// qd holding row qd, transposed in place: afterwards lane qd holds column qd
+// (v[j] = what lane j held in v[qd]).  Two rounds of DPP exchanges (lanes
+// qd ^ 2, then qd ^ 1); moves only, the values are not altered.
+__device__ __forceinline__ void quad_transpose(float (&v)[4], int qd) {
+  const bool lo = (qd & 2) == 0;
+  const float s0 = lo ? v[2] : v[0], s1 = lo ? v[3] : v[1];
+  const float r0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s0), 0x4E, 0xf, 0xf, false));
+  const float r1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s1), 0x4E, 0xf, 0xf, false));
+  if (lo) {
+    v[2] = r0;
+    v[3] = r1;
+  } else {
+    v[0] = r0;
+    v[1] = r1;
+  }
+  const bool ev = (qd & 1) == 0;
+  const float t0 = ev ? v[1] : v[0], t1 = ev ? v[3] : v[2];
+  const float u0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t0), 0xB1, 0xf, 0xf, false));
+  const float u1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t1), 0xB1, 0xf, 0xf, false));
+  if (ev) {
+    v[1] = u0;
+    v[3] = u1;
+  } else {
+    v[0] = u0;
+    v[2] = u1;
+  }
+}
+
 // The tile's outputs.  C[i][j] of a 32 x 32 MFMA block sits in lane
-// j + 32 * (i / 4 % 2), register 4 * (i / 8) + i % 4.  Gate/up: h rows in
+// j + 32 * (i / 4 % 2), register 4 * (i / 8) + i % 4: lane (m, h) holds column
+// m, rows 8 k + 4 h + q in registers 4 k + q.  A 4 x 4 transpose inside each
+// quad of lanes (m = 4 c + q') gives lane q' of the quad row 8 k + 4 h + q',
+// columns 4 c .. 4 c + 3: one 8-byte (bf16) or 16-byte (fp32) store where the
+// MFMA layout needs four (scattered 2- and 4-byte stores took 20-30 k cycles a
+// 256 x 256 tile and slowed the loads queued behind them).  Gate/up: h rows in
 // bf16, silu(gate) * up of the two blocks; down: fp32 rows.
 template <int BM, int NPROJ>
 __device__ __forceinline__ void store_tile(const GemmProblem& P, const TileRef& t, const f32x16 (&acc)[BM / 32][2],
                                            int w, int m, int h) {
+  const int qd = m & 3;
 #pragma unroll
   for (int ib = 0; ib < BM / 32; ++ib) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 32 * ib + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (row >= t.rows) continue;
+    for (int k = 0; k < 4; ++k) {
+      const int row = 32 * ib + 8 * k + 4 * h + qd;
+      const bool live = row < t.rows;
       const int64_t orow = (int64_t)(t.pos0 + row);
       if constexpr (NPROJ == 2) {
-        const int col = t.n0 + 32 * w + m;
-        if (col < P.N) stg(P.outb + orow * P.ldo + col, f32_to_bf16_rne(swiglu_fast(acc[ib][0][r], acc[ib][1][r])));
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = swiglu_fast(acc[ib][0][4 * k + q], acc[ib][1][4 * k + q]);
+        quad_transpose(v, qd);
+        const int col = t.n0 + 32 * w + (m & ~3);
+        if (live && col < P.N) {
+          const uint64_t o = (uint64_t)f32_to_bf16_rne(v[0]) | ((uint64_t)f32_to_bf16_rne(v[1]) << 16) |
+                             ((uint64_t)f32_to_bf16_rne(v[2]) << 32) | ((uint64_t)f32_to_bf16_rne(v[3]) << 48);
+          *(UOCR_GLOBAL uint64_t*)(P.outb + orow * P.ldo + col) = o;
+        }
       } else {
-        const int col = t.n0 + 64 * w + m;
-        if (col < P.N) stg(P.outf + orow * P.ldo + col, acc[ib][0][r]);
-        if (col + 32 < P.N) stg(P.outf + orow * P.ldo + col + 32, acc[ib][1][r]);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = acc[ib][b][4 * k + q];
+          quad_transpose(v, qd);
+          const int col = t.n0 + 64 * w + 32 * b + (m & ~3);
+          if (live && col < P.N) *(UOCR_GLOBAL f32x4*)(P.outf + orow * P.ldo + col) = f32x4{v[0], v[1], v[2], v[3]};
+        }
       }
     }
   }

@@ -313,5 +313,8 @@ hipError_t fused_grid(size_t lds_bytes, int* grid);
 bool fused_trace_built();  // the kernel was compiled with its phase trace (UOCR_DECODE_TRACE=1)
 hipError_t launch_decode_fused(const FusedArgs& a, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_zero_words(uint32_t* p, int64_t n, hipStream_t s);
+// flag[0] = 1 if the error word of the control words at ctl_a or ctl_b (either
+// may be null) is set, else 0; stream-ordered, one tiny kernel.
+hipError_t launch_error_status(uint32_t* flag, const uint32_t* ctl_a, const uint32_t* ctl_b, hipStream_t s);
 
 }  // namespace uocr

@@ -114,7 +114,10 @@ hipError_t own_workspace(hipStream_t stream, size_t bytes, void** out) {
       b.ptr = nullptr;
       b.bytes = 0;
     }
-    const size_t grow = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    // the next power of two (at least 1 MiB): a rising series of sizes retires
+    // less than the live buffer in all, however long it runs
+    size_t grow = size_t(1) << 20;
+    while (grow < bytes) grow <<= 1;
     e = hipMalloc(&b.ptr, grow);
     if (e != hipSuccess) return e;
     b.bytes = grow;
@@ -272,9 +275,12 @@ hipError_t fused_stack_arena(hipStream_t stream, uint64_t** out, bool* need_allo
 }
 
 // Eager persistent launches need the whole device: one on another stream than
-// the previous one first waits for everything queued on that stream.
-hipError_t fused_order(hipStream_t stream) {
-  if (capturing(stream)) return hipSuccess;
+// the previous one first waits for everything queued on that stream.  The
+// wait and the launch are enqueued under one lock, so that the next launch's
+// wait (made by any thread) is recorded after this launch.
+template <typename Launch>
+hipError_t fused_ordered_launch(hipStream_t stream, Launch&& launch) {
+  if (capturing(stream)) return launch();
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -286,8 +292,9 @@ hipError_t fused_order(hipStream_t stream) {
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, d.handoff, 0);
     if (e != hipSuccess) return e;
   }
-  d.last_stream = stream;
-  return hipSuccess;
+  e = launch();
+  if (e == hipSuccess) d.last_stream = stream;
+  return e;
 }
 
 hipError_t fused_grid_cached(size_t lds_bytes, int* grid) {
@@ -988,7 +995,6 @@ static int decode_rows_impl(const char* op, float* out, const float* x, int64_t 
                     "%s: no free control slot for a new stream under capture (make a decode call on this device "
                     "outside stream capture first; it keeps a spare slot ready)",
                     op);
-      if (e == hipSuccess) e = fused_order(s);
     }
     int grid = 0;
     if (e == hipSuccess) e = fused_grid_cached(lay.lds_bytes, &grid);
@@ -1018,7 +1024,11 @@ static int decode_rows_impl(const char* op, float* out, const float* x, int64_t 
         g_trace_grid = grid;
       }
     }
-    e = launch_decode_fused(a, grid, lay.lds_bytes, s);
+    // the static scratch's calls are not ordered (overlapping calls race, as documented)
+    if (fixed != nullptr)
+      e = launch_decode_fused(a, grid, lay.lds_bytes, s);
+    else
+      e = fused_ordered_launch(s, [&] { return launch_decode_fused(a, grid, lay.lds_bytes, s); });
     return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
   }
   Carve dry(nullptr);
@@ -1212,7 +1222,6 @@ int uocr_moe_decode_stack(float* out, const float* x, int64_t rows, int64_t hidd
   if (e == hipSuccess && need_alloc)
     return fail(err, errlen, "%s: no arena for a new stream under capture (make a stacked call on this stream "
                 "outside stream capture first)", op);
-  if (e == hipSuccess) e = fused_order(s);
   int grid = 0;
   if (e == hipSuccess) e = fused_grid_cached(lay.lds_bytes, &grid);
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
@@ -1235,7 +1244,7 @@ int uocr_moe_decode_stack(float* out, const float* x, int64_t rows, int64_t hidd
   a.out = out;
   a.ids_out = nullptr;
   a.wts_out = nullptr;
-  e = launch_decode_fused(a, grid, lay.lds_bytes, s);
+  e = fused_ordered_launch(s, [&] { return launch_decode_fused(a, grid, lay.lds_bytes, s); });
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
 
@@ -1424,11 +1433,15 @@ int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errl
   for (size_t i = 0; e == hipSuccess && i < areas.size(); ++i)
     e = hipMemcpyAsync(&v[i], areas[i].first + C_ERR_WORD, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
-  // a failed launch leaves its slot poisoned (outputs NaN): clear it, control words and tags alike
+  // A failed launch leaves the error word set, and every later launch on the
+  // slot writes NaN until it is cleared.  Only that word is cleared: the
+  // failed launch still counted its arrivals and advanced the epoch, so the
+  // tags it wrote (in the slot's arena and in the stream's stacked-launch
+  // arena) are older than any later launch's, and no wait can take them.
   bool cleared = false;
   for (size_t i = 0; e == hipSuccess && i < areas.size(); ++i) {
     if (v[i] != 0u) {
-      e = launch_zero_words(areas[i].first, areas[i].second, s);
+      e = launch_zero_words(areas[i].first + C_ERR_WORD, 1, s);
       cleared = true;
     }
   }
@@ -1436,6 +1449,29 @@ int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errl
   if (e != hipSuccess) return hip_fail(err, errlen, "uocr_moe_fused_errors", e);
   if (errors) *errors = (v[0] | v[1]) != 0u ? 1u : 0u;
   return 0;
+}
+
+int uocr_moe_fused_status(uint32_t* flag, void* stream, char* err, size_t errlen) {
+  const char* op = "uocr_moe_fused_status";
+  if (flag == nullptr) return fail(err, errlen, "%s: no flag", op);
+  const hipStream_t s = (hipStream_t)stream;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(err, errlen, op, e);
+  const uint32_t* slot = nullptr;
+  const uint32_t* fixed = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_fused.find(dev);
+    if (it != g_fused.end()) {
+      auto sl = it->second.slot.find(s);
+      if (sl != it->second.slot.end()) slot = sl->second.ctl;
+    }
+    auto sc = g_scratch.find(dev);
+    if (sc != g_scratch.end()) fixed = reinterpret_cast<const uint32_t*>(sc->second);
+  }
+  e = launch_error_status(flag, slot, fixed, s);
+  return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
 
 void uocr_moe_release(void) {

@@ -11,7 +11,7 @@ guard) and the decode step they make up (:mod:`uocr_moe.decoder`).
 from ._lib import LIB_PATH, UocrError
 from .checkpoint import WeightMappingError, load_safetensors, moe_from_checkpoint, moe_layer_weights
 from .decoder import Decoder, DecoderConfig, DecoderLayer, rope_tables
-from .moe import MoE, MoeConfig, decode_stack, gate
+from .moe import MoE, MoeConfig, decode_stack, fused_status, gate
 from .ops import (
     PagedKv,
     custom,
@@ -43,6 +43,7 @@ __all__ = [
     "custom",
     "decode_stack",
     "dense_bf16_qmv",
+    "fused_status",
     "gate",
     "int8_dequant_expert",
     "kblocked",

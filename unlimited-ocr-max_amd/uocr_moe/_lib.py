@@ -70,6 +70,7 @@ SIGNATURES: dict[str, list] = {
     "uocr_moe_release": [],
     "uocr_moe_timing_begin": [_int, _cp, _sz],
     "uocr_moe_fused_errors": [_vp, ctypes.POINTER(ctypes.c_uint32), _cp, _sz],
+    "uocr_moe_fused_status": [_vp, _vp, _cp, _sz],
     "uocr_moe_fused_trace": [_vp, _i64, ctypes.POINTER(_int), _cp, _sz],
     "uocr_moe_timing_end": [_int, _vp, _vp, _sz, ctypes.POINTER(_int), _cp, _sz],
 }

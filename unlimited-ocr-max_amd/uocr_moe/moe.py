@@ -126,9 +126,17 @@ class MoE:
                   workspace.data_ptr(), workspace.numel(), _stream(x))
         return (out, ids, wts) if routing else out
 
-    def decode_rows(self, x: torch.Tensor, *, workspace: torch.Tensor | None = None, routing: bool = False):
-        """MoE.decode_rows (decoder.py:641-655): row ``b`` of ``x [B, H]`` is request ``b``'s token."""
-        return self._run("uocr_moe_decode_rows", x, False, workspace, routing)
+    def decode_rows(self, x: torch.Tensor, *, workspace: torch.Tensor | None = None, routing: bool = False,
+                    status: torch.Tensor | None = None):
+        """MoE.decode_rows (decoder.py:641-655): row ``b`` of ``x [B, H]`` is request ``b``'s token.
+
+        ``status`` (optional, an int32 device tensor of at least one element) receives, in stream order
+        after the launch, 1 if the persistent decode kernel's bounded waits ran out on this stream (its
+        outputs are then NaN) and 0 otherwise; no synchronisation (see :func:`fused_status`)."""
+        out = self._run("uocr_moe_decode_rows", x, False, workspace, routing)
+        if status is not None:
+            fused_status(status)
+        return out
 
     def __call__(self, x: torch.Tensor, *, workspace: torch.Tensor | None = None, routing: bool = False):
         """MoE.__call__ (decoder.py:657-667): the prefill over ``x [seq, H]``."""
@@ -139,11 +147,11 @@ class MoE:
         return gate(x, self.router, self.config.num_experts_per_tok, renormalize=self.config.renormalize)
 
 
-def decode_stack(layers: "list[MoE]", x: torch.Tensor) -> torch.Tensor:
+def decode_stack(layers: "list[MoE]", x: torch.Tensor, *, status: torch.Tensor | None = None) -> torch.Tensor:
     """The MoE blocks of consecutive decoder layers on the residual stream, one launch:
     ``x_{l+1} = x_l + layers[l].decode_rows(x_l)`` (the adds of decoder.py:709 with the attention
     taken out), returning ``x_n``; the same bits as chaining ``decode_rows``.  Up to 12 layers of
-    one shape and kind, ``x [B, H]`` with B <= 8."""
+    one shape and kind, ``x [B, H]`` with B <= 8.  ``status`` as for :meth:`MoE.decode_rows`."""
     op = "uocr_moe_decode_stack"
     x = _gpu(op, "x", x, torch.float32, 2)
     if not layers:
@@ -151,7 +159,21 @@ def decode_stack(layers: "list[MoE]", x: torch.Tensor) -> torch.Tensor:
     out = torch.empty_like(x)
     ptrs = (ctypes.POINTER(_lib.Layer) * len(layers))(*[ctypes.pointer(m._layer) for m in layers])
     _lib.call(op, out.data_ptr(), x.data_ptr(), int(x.shape[0]), int(x.shape[1]), ptrs, len(layers), _stream(x))
+    if status is not None:
+        fused_status(status)
     return out
+
+
+def fused_status(flag: torch.Tensor) -> torch.Tensor:
+    """Writes ``flag[0]`` on the device, in stream order: 1 if a persistent decode launch on the current
+    stream (or on the device's static scratch) ran out of its bounded waits, else 0.  Nothing is
+    synchronised or cleared (``uocr_moe._lib.fused_errors`` reports with a sync and resets the slot);
+    the reference's ops fail on the host only (kernels/moe_int8.mojo:194-210)."""
+    op = "uocr_moe_fused_status"
+    if not (flag.is_cuda and flag.dtype == torch.int32 and flag.numel() >= 1 and flag.is_contiguous()):
+        raise ValueError(f"{op}: flag must be a contiguous int32 device tensor of at least one element")
+    _lib.call(op, flag.data_ptr(), _stream(flag))
+    return flag
 
 
 def gate(x: torch.Tensor, router: torch.Tensor, top_k: int, *, renormalize: bool = False):
