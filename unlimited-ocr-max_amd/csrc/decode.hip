@@ -251,9 +251,13 @@ __device__ __forceinline__ int task_count(const KA FusedArgs& A, int ng) {
 }
 
 // Tasks before the routed ones: the router, and the shared gate/up partials
-// (which wait for nothing).  The shared folds and down partials, which wait
-// for the sgu partials, follow the routed gate/up tasks.
-__device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.E + A.n_sgu; }
+// (which wait for nothing); at small batches (early_shared) also the shared
+// folds and down partials, which wait for the sgu partials.  Otherwise these
+// follow the routed gate/up tasks (at B=8 their waves are better spent on
+// routed tasks: 49.8 against 55.0 us a layer).
+__device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) {
+  return A.E + A.n_sgu + (A.early_shared ? A.n_sfold + A.n_sdn : 0);
+}
 
 // x / d from m = ceil(2^32 / d) (0 for d = 1), exact while x * d < 2^32: a
 // multiply-high in place of an integer division's ~40 dependent instructions,
@@ -262,8 +266,9 @@ __device__ __forceinline__ int unrouted_count(const KA FusedArgs& A) { return A.
 // kept its division, which measured faster there).
 __device__ __forceinline__ int task_div(int x, uint32_t m) { return m ? (int)__umulhi((uint32_t)x, m) : x; }
 
-// Task order: router, sgu, rgu, sfold, sdn, rdn, comb (every task waits only
-// for tasks before it).
+// Task order: router, sgu, rgu, sfold, sdn, rdn, comb, or at small batches
+// (early_shared) router, sgu, sfold, sdn, rgu, rdn, comb (either way every
+// task waits only for tasks before it).
 __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
   if (t < A.E) return {K_ROUTER, t, 0, 0};
   t -= A.E;
@@ -274,11 +279,14 @@ __device__ __forceinline__ Task task_at(const KA FusedArgs& A, int ng, int t) {
     return {K_SGU, u, p, r - p * A.gh};
   }
   t -= A.n_sgu;
-  if (t < ng * A.per_e_gu) {
-    const int s = task_div(t, A.m_gu);
-    return {K_RGU, s, t - s * A.per_e_gu, 0};
+  // the routed gate/up tasks' place: first, or after the shared folds and downs
+  const int n_gu = ng * A.per_e_gu;
+  const int gu0 = A.early_shared ? A.n_sfold + A.n_sdn : 0;
+  if (t >= gu0 && t < gu0 + n_gu) {
+    const int s = task_div(t - gu0, A.m_gu);
+    return {K_RGU, s, t - gu0 - s * A.per_e_gu, 0};
   }
-  t -= ng * A.per_e_gu;
+  if (t >= gu0) t -= n_gu;
   if (t < A.n_sfold) {
     const int u = task_div(t, A.m_b);
     return {K_SFOLD, u, t - u * A.B, 0};
@@ -332,7 +340,8 @@ __device__ __forceinline__ uint64_t slot_rows(const Route& rt, int e) {
 // tables (same steps as route.hip's k_softmax_topk: max, exp, halving-tree
 // sum, divide; the k largest probabilities in turn, ties to the lower id),
 // then one more on the workgroup's count of routed tokens.
-__device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int64_t boff, int t, uint32_t tag,
+__device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A, int64_t boff, int64_t twg, int t,
+                                                           uint32_t tag,
                                                            int* r_ids,
                                                            float* r_wts, int* r_done, uint64_t* keys) {
   const int l = lane();
@@ -340,18 +349,18 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   uint64_t q;
   uint32_t spin = A.spin_limit;
   const bool wtrace = kTrace && A.trace != nullptr && t == 0 && l == 0;
-  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 0] = (int64_t)wall_clock64();
+  if (wtrace) A.trace[twg + blockIdx.x * 8 + 0] = (int64_t)wall_clock64();
   do {
     q = ld_pair(src);
   } while (!poll_done(pair_has(q, tag), spin, A.ctl));
-  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 1] = (int64_t)wall_clock64();
+  if (wtrace) A.trace[twg + blockIdx.x * 8 + 1] = (int64_t)wall_clock64();
   const bool real = l < A.E;
   const float v = real ? (expired(spin) ? __builtin_nanf("") : pair_value(q)) : -__builtin_huge_valf();
   const float m = tree_max(v);
-  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 3] = (int64_t)wall_clock64();
+  if (wtrace) A.trace[twg + blockIdx.x * 8 + 3] = (int64_t)wall_clock64();
   const float ex = real ? uexp(v - m) : 0.0f;
   const float S = tree_sum(ex);
-  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 4] = (int64_t)wall_clock64();
+  if (wtrace) A.trace[twg + blockIdx.x * 8 + 4] = (int64_t)wall_clock64();
   const float pr = real ? ex / S : 0.0f;
   // The k largest probabilities in turn, ties to the lower id, as ranks: lane
   // l's key ((bits of pr) << 6 | 63 - l) + 1 (0 past the experts) is distinct
@@ -387,7 +396,7 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
       if (j < A.topk) d = d + wv[j];
     my_w = pr / d;
   }
-  if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 5] = (int64_t)wall_clock64();
+  if (wtrace) A.trace[twg + blockIdx.x * 8 + 5] = (int64_t)wall_clock64();
   if (chosen) {
     const int i = t * A.topk + rank;
     r_ids[i] = l;
@@ -401,7 +410,7 @@ __device__ __attribute__((always_inline)) void route_token(const KA FusedArgs& A
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   if (l == 0) {
     __hip_atomic_fetch_add(r_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (wtrace) A.trace[A.trace_wg + blockIdx.x * 8 + 2] = (int64_t)wall_clock64();
+    if (wtrace) A.trace[twg + blockIdx.x * 8 + 2] = (int64_t)wall_clock64();
   }
 }
 
@@ -538,7 +547,9 @@ struct Ctx {
   const float* r_wts;
   float* act;       // the wave's activation stage
   uint32_t tag;
-  int t;            // the running task (tracing)
+  int* landed;      // the workgroup's routed gate/up tasks whose weights have landed (LDS; defer_down)
+  int t;            // the running task
+  int tr;           // its trace record: t, plus the layer's offset in a stack
   int layer;        // the layer of a stack (0 for one layer)
   int64_t boff;     // the layer's tagged buffers, in words from the first layer's
   const KA FusedLayerW* W;  // the layer's weights
@@ -598,7 +609,7 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
       if ((l & 15) == 0 && tt < t1) st_pair_xcd(dst + tt * 64, v[0], C.tag);
     }
   }
-  if (t0 == 0) UOCR_TRACE(A, C.t, 4);
+  if (t0 == 0) UOCR_TRACE(A, C.tr, 4);
 }
 
 // Shared gate or up, 64 columns x chunk g of H, every token: partials.
@@ -614,7 +625,7 @@ __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, c
 __device__ __attribute__((always_inline)) void task_sgu(const KA FusedArgs& A, const Ctx& C, const Task& k) {
   Stage<false> st;
   issue_kblocked(k.b ? C.W->sh_up : C.W->sh_gate, A.Fs, k.a * 64, k.c, st);
-  UOCR_TRACE_LOADS(A, C.t);
+  UOCR_TRACE_LOADS(A, C.tr);
   sgu_rows(A, C, k, st);
 }
 
@@ -637,7 +648,7 @@ __device__ __attribute__((always_inline)) void task_sfold(const KA FusedArgs& A,
       if (g < A.gh) sum = sum + v[g];
     acc[p] = sum;
   }
-  UOCR_TRACE(A, C.t, 3);
+  UOCR_TRACE(A, C.tr, 3);
   st_pair(A.hs + C.boff + (int64_t)r * A.Fs + k.a * 64 + l, silu(acc[0]) * acc[1], C.tag);
 }
 
@@ -647,7 +658,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   const int g = k.b;
   Stage<false> st;
   issue_kblocked(C.W->sh_down, A.H, k.a * 64, g, st);
-  UOCR_TRACE_LOADS(A, C.t);
+  UOCR_TRACE_LOADS(A, C.tr);
   // hs[r][g*128 .. +128) of every token into the activation stage (row r at r*128)
   {
     // pair i is row i/2, element (i%2)*64 + l; the first pair is probed first
@@ -684,7 +695,7 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
       if (i < np) C.act[(i >> 1) * 128 + (i & 1) * 64 + l] = v[i];
     __builtin_amdgcn_wave_barrier();
   }
-  UOCR_TRACE(A, C.t, 3);
+  UOCR_TRACE(A, C.tr, 3);
   uint64_t* dst = A.p_sdn + C.boff + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
   for (int r = 0; r < A.B; ++r) {
     launder(st);
@@ -767,7 +778,12 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
       }
     }
   }
-  UOCR_TRACE_LOADS(A, C.t);
+  UOCR_TRACE_LOADS(A, C.tr);
+  if (A.defer_down) {
+    // the weights and scales have landed: the workgroup's down tasks may issue theirs
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane() == 0) __hip_atomic_fetch_add(C.landed, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
 #pragma unroll
   for (int j = 0; j < SUB; ++j) {
     if (bk.ncols[j] <= 0) break;
@@ -791,11 +807,30 @@ __device__ __attribute__((always_inline)) void task_rgu(const KA FusedArgs& A, c
       const int tok = STACK ? r / A.topk : small_div(r, __builtin_amdgcn_rcpf((float)A.topk));
       const float part = chain<INT8>(bk.st[j], C.xs + (tok * A.gh + g) * kXPad);
       const float acc = fold_groups<INT8, kMaxG, STACK>(part, bk.scale[j], base, A.gh);
-      UOCR_TRACE(A, C.t, 4);
+      UOCR_TRACE(A, C.tr, 4);
       const float up = shfl(acc, min(l + A.gh, kWave - 1));
       if (writer) st_pair(A.h + C.boff + (int64_t)r * A.F + n0 + c, silu(acc) * up, C.tag);
     }
   }
+}
+
+// defer_down: waits until the routed gate/up tasks that the workgroup's waves
+// took first have their weights landed (they wait only for the routing, so
+// the count is reached), for at most kDeferTicks of the wall clock.
+constexpr int64_t kDeferTicks = 1000;  // 10 us at 100 MHz
+__device__ __forceinline__ void defer_for_gate_up(const KA FusedArgs& A, const Ctx& C, const Route& rt) {
+  const int gu0 = unrouted_count(A);
+  const int gu1 = gu0 + rt.ng * A.per_e_gu;
+  int want = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = A.E + w * (int)gridDim.x + (int)blockIdx.x;
+    want += (t >= gu0 && t < gu1) ? 1 : 0;
+  }
+  const int64_t end = (int64_t)wall_clock64() + kDeferTicks;
+  while (__hip_atomic_load(C.landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < want &&
+         (int64_t)wall_clock64() < end)
+    __builtin_amdgcn_s_sleep(1);
 }
 
 // Routed down of one expert for SUB blocks of c_dn columns, every chunk of F,
@@ -810,6 +845,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
   const int l = lane();
   const int e = slot_expert(rt, k.a);
   uint64_t rows = slot_rows(rt, e);
+  if (A.defer_down) defer_for_gate_up(A, C, rt);
   Blocks<INT8, SUB> bk;
 #pragma unroll
   for (int j = 0; j < SUB; ++j) {
@@ -825,7 +861,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
       }
     }
   }
-  UOCR_TRACE_LOADS(A, C.t);
+  UOCR_TRACE_LOADS(A, C.tr);
   const int npairs = A.F / kWave;  // pairs of one h row per lane: element l + 64 i
   while (rows != 0ull) {
     const int r = (int)__builtin_ctzll(rows);
@@ -851,7 +887,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
       }
     }
     __builtin_amdgcn_wave_barrier();
-    UOCR_TRACE(A, C.t, 3);
+    UOCR_TRACE(A, C.tr, 3);
 #pragma unroll
     for (int j = 0; j < SUB; ++j) {
       if (bk.ncols[j] <= 0) break;
@@ -862,7 +898,7 @@ __device__ __attribute__((always_inline)) void task_rdn(const KA FusedArgs& A, c
       launder(bk.st[j]);
       const float part = chain<INT8>(bk.st[j], C.act + g * kXPad);
       const float acc = fold_groups<INT8, kMaxG, STACK>(part, bk.scale[j], c * A.gf, A.gf);
-      UOCR_TRACE(A, C.t, 4);
+      UOCR_TRACE(A, C.tr, 4);
       if (g == 0 && l < lanes) st_pair(A.y + C.boff + (int64_t)r * A.H + bk.n0[j] + c, acc, C.tag);
     }
     __builtin_amdgcn_wave_barrier();
@@ -889,7 +925,7 @@ __device__ __attribute__((always_inline)) void task_comb(const KA FusedArgs& A, 
   float y[kMaxK];
   poll_pairs<kMaxK, kPollFull>(A.y + C.boff + (int64_t)t * A.topk * A.H + n, A.H, A.topk, C.tag, A.ctl,
                                A.spin_limit, y);
-  UOCR_TRACE(A, C.t, 3);
+  UOCR_TRACE(A, C.tr, 3);
   float wj[kMaxK];
 #pragma unroll
   for (int j = 0; j < kMaxK; ++j) wj[j] = C.r_wts[t * A.topk + min(j, A.topk - 1)];
@@ -917,10 +953,11 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
                                                         const Task& k, int64_t troute) {
   Ctx C = C0;
   C.t = t;
-  UOCR_TRACE(A, t, 0);
+  C.tr = kTrace ? t + C.layer * (int)A.trace_layer : t;
+  UOCR_TRACE(A, C.tr, 0);
   if (kTrace && A.trace != nullptr && lane() == 0) {
-    A.trace[(int64_t)t * 8 + 5] = troute;
-    A.trace[(int64_t)t * 8 + 6] = k.kind;
+    A.trace[(int64_t)C.tr * 8 + 5] = troute;
+    A.trace[(int64_t)C.tr * 8 + 6] = k.kind;
   }
   switch (k.kind) {
     case K_SGU: task_sgu(A, C, k); break;
@@ -936,9 +973,9 @@ __device__ __attribute__((always_inline)) void run_task(const KA FusedArgs& A, c
     case K_COMB: task_comb(A, C, k); break;
     default: break;
   }
-  UOCR_TRACE(A, t, 2);
+  UOCR_TRACE(A, C.tr, 2);
   if (kTrace && A.trace != nullptr && lane() == 0)
-    A.trace[(int64_t)t * 8 + 7] = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+    A.trace[(int64_t)C.tr * 8 + 7] = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
 }
 
 // One instantiation per routed weight type, each with its own register
@@ -956,6 +993,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
   int* r_ids = (int*)(lds + A.lds_x);
   float* r_wts = (float*)(lds + A.lds_x + 256);
   int* r_done = (int*)(lds + A.lds_x + 512);  // tokens routed so far
+  C.landed = (int*)(lds + A.lds_x + 520);
   C.xs = xs;
   C.r_ids = r_ids;
   C.r_wts = r_wts;
@@ -998,6 +1036,8 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     const KA FusedArgs& A = *Al;
     C.layer = layer;
     C.boff = (int64_t)layer * A.layer_words;
+    // this layer's per-workgroup trace records
+    const int64_t twg = kTrace ? A.trace_wg + (int64_t)layer * A.trace_layer * 8 : 0;
     C.W = &A.w[layer];
     int t = A.E + rank;
 
@@ -1019,6 +1059,9 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
       const int n = A.B * A.H;
       const uint64_t* src = A.xs_pairs + (int64_t)(layer - 1) * n;
       uint32_t spin = A.spin_limit;
+      // (traced: the layer's start, every wave done with the previous one, as the epoch-read record)
+      if (kTrace && A.trace != nullptr && threadIdx.x == kCtlThread)
+        A.trace[twg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
       for (;;) {
         bool ok = true;
 #pragma unroll
@@ -1034,6 +1077,9 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
         }
         if (poll_done(ok, spin, A.ctl)) break;
       }
+      // (traced: the control wave's x landed, as the entry record)
+      if (kTrace && A.trace != nullptr && threadIdx.x == kCtlThread)
+        A.trace[twg + blockIdx.x * 8 + 6] = (int64_t)wall_clock64();
       if (expired(spin)) {
         for (int i = tid; i < n; i += kThreads) {
           const int r = task_div(i, A.m_h);
@@ -1077,11 +1123,12 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     // first waves.
     if (threadIdx.x == kCtlThread) {
       *r_done = 0;
+      *C.landed = 0;
       if (layer == 0) {
         *lds_epoch = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
         if (kTrace && A.trace != nullptr) {
           asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-          A.trace[A.trace_wg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
+          A.trace[twg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();
         }
       }
     }
@@ -1099,18 +1146,19 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
       // the trace keeps one record per expert: XCD 0's task of its first tokens
       const bool traced = r_t0 == 0 && blockIdx.x % kXcds == 0;
       C.t = r_e;
-      if (traced) UOCR_TRACE(A, r_e, 0);
-      if (traced) UOCR_TRACE_LOADS(A, r_e);
+      C.tr = kTrace ? r_e + layer * (int)A.trace_layer : r_e;
+      if (traced) UOCR_TRACE(A, C.tr, 0);
+      if (traced) UOCR_TRACE_LOADS(A, C.tr);
       router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
-      if (traced) UOCR_TRACE(A, r_e, 2);
-      if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)r_e * 8 + 7] = rank;
+      if (traced) UOCR_TRACE(A, C.tr, 2);
+      if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)C.tr * 8 + 7] = rank;
     }
     // The routing of token i is computed by wave kWaves-1-i (high waves, whose
     // tasks come late in the list); the other waves meanwhile run their tasks
     // that do not need the routing (the shared experts).
     const int rwave = kWaves - 1 - wave;
     // (the routing wave's activation stage, idle until its first task, holds the keys)
-    if (rwave < A.B) route_token(A, C.boff, rwave, C.tag, r_ids, r_wts, r_done, (uint64_t*)C.act);
+    if (rwave < A.B) route_token(A, C.boff, twg, rwave, C.tag, r_ids, r_wts, r_done, (uint64_t*)C.act);
     // One task loop (one copy of the task code): the first routed task waits
     // for the workgroup's routing.
     Route rt{0ull, 0, r_ids, 0};

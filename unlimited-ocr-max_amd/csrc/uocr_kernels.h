@@ -230,6 +230,10 @@ constexpr int kFusedCtlWords = 2368;      // control words per slot: error word,
 constexpr int kFusedXcds = 8;              // XCDs of the device (workgroup b runs on XCD b % 8)
 constexpr int kFusedLogitCopies = kFusedXcds;  // copies of the tagged logits, one per XCD
 constexpr int kFusedRouterWaves = 4;       // router tasks per workgroup
+#ifndef UOCR_EARLY_SHARED_ROWS
+#define UOCR_EARLY_SHARED_ROWS 1
+#endif
+constexpr int kFusedEarlySharedRows = UOCR_EARLY_SHARED_ROWS;  // batches up to this size use early_shared, defer_down
 constexpr int kFusedLogitCopyWords = 576;  // 64-bit words per copy (8 tokens x 64 experts, padded)
 
 // Task layout, LDS and tagged-buffer sizes of one layer shape.
@@ -304,10 +308,19 @@ struct FusedArgs {
   uint32_t spin_limit;
   int r_tok;  // tokens per router task
   int x_vec;  // x is 16-byte aligned
+  // small batches: the shared fold and down tasks come before the routed
+  // ones (their weights stream while the routing is computed), and a routed
+  // down task issues its weights once its workgroup's routed gate/up weights
+  // have landed (the gate/up weights, which the next step waits for, then
+  // have the memory to themselves)
+  int early_shared;
+  int defer_down;
   // optional per-task phase timestamps (8 words per task), null when off;
-  // per-workgroup words start at trace_wg
+  // per-workgroup words start at trace_wg; a stack's layer l has its records
+  // trace_layer records (of 8 words) after layer 0's
   int64_t* trace;
   int64_t trace_wg;
+  int64_t trace_layer;
 };
 hipError_t fused_grid(size_t lds_bytes, int* grid);
 bool fused_trace_built();  // the kernel was compiled with its phase trace (UOCR_DECODE_TRACE=1)

@@ -898,6 +898,8 @@ static FusedArgs fused_args(const uocr_moe_layer* L, int64_t B, const FusedLayou
   a.m_b = magic(B);
   a.m_gfs = magic(lay.gfs);
   a.m_dn = magic(lay.per_e_dn);
+  a.early_shared = B <= kFusedEarlySharedRows ? 1 : 0;
+  a.defer_down = B <= kFusedEarlySharedRows ? 1 : 0;
   a.m_h = magic(a.H);
   a.spin_limit = fused_spin_limit();
   return a;
@@ -1244,6 +1246,17 @@ int uocr_moe_decode_stack(float* out, const float* x, int64_t rows, int64_t hidd
   a.out = out;
   a.ids_out = nullptr;
   a.wts_out = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    const int64_t per_layer = (int64_t)lay.max_tasks + grid;  // records of one layer
+    if (g_trace != nullptr && g_trace_words >= per_layer * n_layers * 8) {
+      a.trace = g_trace;
+      a.trace_wg = (int64_t)lay.max_tasks * 8;
+      a.trace_layer = per_layer;
+      g_trace = nullptr;
+      g_trace_grid = grid;
+    }
+  }
   e = fused_ordered_launch(s, [&] { return launch_decode_fused(a, grid, lay.lds_bytes, s); });
   return e == hipSuccess ? 0 : hip_fail(err, errlen, op, e);
 }
