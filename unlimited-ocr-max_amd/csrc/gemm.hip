@@ -888,23 +888,145 @@ __device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t,
   store_tile<32 * NACT, NPROJ>(P, t, acc, w, m, h);
 }
 
-// Placement for the LDS-staged path.  A unit is one column tile of one
-// group and a run of its row tiles (a routed expert's unit has all of them,
-// so each expert weight tile is fetched into one L2 and serves all of its
-// rows there; the shared experts' many row tiles are cut into at most 8
-// runs).  Units are dealt round robin to the XCDs (routed first, the shared
-// ones numbered on): an expert's 5-8 column tiles land on as many XCDs, so a
-// hot expert is spread over the chip.
+// Placement for the LDS-staged path, two ways, chosen per launch from the
+// rows (the tile count it bounds).
 //
-// Order.  A tile's cost grows with its active 32-row blocks, and an int8
-// tile's much more than a bf16 one's (the dequantisation is paid per tile).
-// An XCD's tiles are listed class by class in decreasing estimated cost
-// (class: problem and active blocks; within a class, unit order), and its
-// workgroup j walks tiles j, j + J, ... of the list: the costly tiles start
-// first and the last round is made of short ones.  (A work queue -- atomic
-// per-XCD counters, tiles taken as workgroups finish them -- measured slower
-// on this GPU: the counter round trips and their broadcast cost more than
-// the balance gained.)
+// Balanced (BAL, launches of several rounds: T = 4096).  The routed tiles
+// form a sequence: the groups from the most rows to the fewest (ties in
+// group order), each row tile by row tile and, within a row tile, column
+// tile by column tile.  The sequence is cut into 8 contiguous ranges of equal
+// estimated cost (a tile belongs to the range its cost midpoint falls in),
+// range x going to XCD x; the shared experts' row tiles are cut into 8 runs
+// of equal length (all their column tiles), run x going to XCD x ahead of
+// its routed range.  Workgroup j of an XCD walks tiles j, j + J, ... of that
+// list.  So every XCD gets the same work whatever the routing (dealing whole
+// (group, column tile) units round robin left the XCDs up to 2x apart with
+// skewed routing: T = 4096 down 144 -> 127 us, adversarial routing 400 ->
+// 358 us a layer), and a group stays on one XCD (two where a range ends
+// inside it): its weight tiles and its gathered A rows are fetched into that
+// XCD's L2 and serve all of the group's row and column tiles there, the row
+// tiles running in order so that the XCD's workgroups share a few row tiles'
+// A at a time.
+//
+// By class (launches of at most two rounds: T = 512, about one tile a
+// workgroup, where the balance of single tiles matters more).  A unit is one
+// column tile of one group and a run of its row tiles (a routed expert's
+// unit has all of them, so each expert weight tile is fetched into one L2
+// and serves all of its rows there; the shared experts' many row tiles are
+// cut into at most 8 runs).  Units are dealt round robin to the XCDs (routed
+// first, the shared ones numbered on).  An XCD's tiles are listed class by
+// class in decreasing estimated cost (class: problem and active blocks;
+// within a class, unit order), and its workgroup j walks tiles j, j + J, ...
+// of the list: the costly tiles start first and the second round is made of
+// the cheapest ones.  (The balanced placement made T = 512 131 -> 151 us: its
+// contiguous ranges put a range's costly tiles in one XCD's second round.)
+//
+// (A work queue -- atomic per-XCD counters, tiles taken as workgroups finish
+// them -- measured slower on this GPU: the counter round trips and their
+// broadcast cost more than the balance gained.)
+//
+// Cost.  A tile's cost grows with its active 32-row blocks, and an int8
+// tile's more than a bf16 one's (the dequantisation is paid per tile).
+// Estimated cost per 64-k step: 100 + 35 per block for int8 weights, 65 + 36
+// per block for bf16, plus 600 a tile for its start and its stores
+// (per-XCD busy times at T = 4096 fit these within about 10 %).
+__device__ __forceinline__ int tile_cost(const GemmProblem& P, int nact) {
+  return (P.K / BK) * (P.kind == kInt8Rows ? 100 + 35 * nact : 65 + 36 * nact) + 600;
+}
+
+// One problem's row tiles: rt in all, the last one partial with `apart`
+// active blocks when part is set.
+struct RowTiles {
+  int rt, part, apart;
+};
+template <int BM>
+__device__ __forceinline__ RowTiles row_tiles_of(int count) {
+  RowTiles r;
+  r.rt = (count + BM - 1) / BM;
+  const int rem = count - (r.rt - 1) * BM;
+  r.part = count > 0 && rem < BM ? 1 : 0;
+  r.apart = r.part ? (rem + 31) >> 5 : 0;
+  return r;
+}
+
+// The routed tile sequence.  Lane p holds the group of rank p (most rows
+// first): the tiles and cost before it, its first row position, rows and
+// expert (ranks past the last group hold no rows).
+struct Seq {
+  int tp, cp, start, count, e;
+  int ta, ca;    // routed tiles and cost
+  int nta, ntb;  // column tiles of each problem
+};
+
+template <int BMA, int BMB>
+__device__ __forceinline__ Seq make_seq(const GemmProblem& a, const GemmProblem& b, int bn) {
+  Seq q;
+  q.nta = (a.N + bn - 1) / bn;
+  q.ntb = (b.N + bn - 1) / bn;
+  const bool routed = a.rows.n_groups != nullptr;
+  const int l = lane_id();
+  // the group tables for every lane at once, clamped to their size, before
+  // the group count is known (one memory latency at the kernel's start)
+  int g0 = 0, g1 = 0, ge = 0;
+  if (routed && a.max_groups > 0) {
+    const int g = min(l, a.max_groups - 1);
+    g0 = ldg(a.rows.group_start + g);
+    g1 = ldg(a.rows.group_start + g + 1);
+    ge = ldg(a.rows.group_expert + g);
+  }
+  const int ng = routed ? ldc(a.rows.n_groups) : (a.M > 0 ? 1 : 0);
+  int start = 0, count = 0, e = 0;
+  if (l < ng) {
+    start = routed ? g0 : 0;
+    count = routed ? g1 - g0 : a.M;
+    e = routed ? ge : 0;
+  }
+  // the group's rank, most rows first (ties in group order; no rows last),
+  // and its values moved to the lane of that rank
+  int rank = 0;
+#pragma unroll 8
+  for (int k = 0; k < kWave; ++k) {
+    const int ck = __builtin_amdgcn_readlane(count, k);
+    rank += (ck > count || (ck == count && k < l)) ? 1 : 0;
+  }
+  q.start = __builtin_amdgcn_ds_permute(rank << 2, start);
+  q.count = __builtin_amdgcn_ds_permute(rank << 2, count);
+  q.e = __builtin_amdgcn_ds_permute(rank << 2, e);
+  const RowTiles r = row_tiles_of<BMA>(q.count);
+  const int tiles = q.nta * r.rt;
+  const int cost = q.nta * ((r.rt - r.part) * tile_cost(a, BMA / 32) + (r.part ? tile_cost(a, r.apart) : 0));
+  const int ti = wave_scan_i(tiles), ci = wave_scan_i(cost);
+  q.tp = ti - tiles;
+  q.cp = ci - cost;
+  q.ta = __builtin_amdgcn_readlane(ti, kWave - 1);
+  q.ca = __builtin_amdgcn_readlane(ci, kWave - 1);
+  return q;
+}
+
+// Tiles of cost c each whose midpoints lie below t (t >= 0): (2i + 1) c < 2t.
+__device__ __forceinline__ int below(int64_t t, int c) {
+  return 2 * t > c ? (int)((2 * t - c + 2 * (int64_t)c - 1) / (2 * (int64_t)c)) : 0;
+}
+// Tiles of one problem's group (its row tiles r, nt columns) whose cost
+// midpoints lie below t (0 <= t <= the group's cost).
+template <int BM>
+__device__ __forceinline__ int group_below(const GemmProblem& P, const RowTiles& r, int nt, int64_t t) {
+  const int cf = tile_cost(P, BM / 32);
+  const int64_t full = (int64_t)nt * (r.rt - r.part) * cf;
+  if (t <= full) return below(t, cf);
+  return nt * (r.rt - r.part) + (r.part ? min(nt, below(t - full, tile_cost(P, r.apart))) : 0);
+}
+// Index of the first routed tile whose cost midpoint is at least t.
+template <int BMA>
+__device__ __forceinline__ int seq_below(const GemmProblem& a, const Seq& q, int64_t t) {
+  if (t <= 0) return 0;
+  if (t >= q.ca) return q.ta;
+  // the last group whose cost starts at or below t (the ranked groups with rows come first)
+  const int g = (int)__popcll(__ballot(q.count > 0 && q.cp <= t)) - 1;
+  const int cp = __builtin_amdgcn_readlane(q.cp, g), tp = __builtin_amdgcn_readlane(q.tp, g);
+  const int count = __builtin_amdgcn_readlane(q.count, g);
+  return tp + group_below<BMA>(a, row_tiles_of<BMA>(count), q.nta, t - cp);
+}
 
 constexpr int kMaxUnits = 1024;  // per problem: 128 per XCD, two a lane
 
@@ -1008,9 +1130,7 @@ __device__ __forceinline__ TileRef class_tile(const GemmProblem& P, const Units&
 
 // The classes of a launch in decreasing estimated cost, and an XCD's tiles
 // of each.  Class k: problem cls[k] >> 8 (0 routed, 1 shared), cls[k] & 255
-// active blocks.  Estimated cost per 64-k step: 100 + 35 per block for int8
-// weights, 45 + 25 per block for bf16 (measured tile times fit these within
-// about 15 %).
+// active blocks, ordered by tile_cost.
 constexpr int kMaxClasses = 6;
 struct Sched {
   int n;
@@ -1018,10 +1138,6 @@ struct Sched {
   int cnt[kMaxClasses];
   int total;
 };
-
-__device__ __forceinline__ int tile_cost(const GemmProblem& P, int nact) {
-  return (P.K / BK) * (P.kind == kInt8Rows ? 100 + 35 * nact : 45 + 25 * nact);
-}
 
 template <int BMA, int BMB>
 __device__ __forceinline__ Sched make_sched(const GemmProblem& a, const GemmProblem& b, const Units& qa,
@@ -1063,9 +1179,81 @@ __device__ __forceinline__ Sched make_sched(const GemmProblem& a, const GemmProb
   return sd;
 }
 
+// The balanced placement's walk of the XCD's list.
 template <WKind W0, int NP>
-__global__ void __launch_bounds__(kGThreads, kWgPerCu) k_moe_gemm_lds(GemmProblem a, GemmProblem b) {
-  extern __shared__ __attribute__((aligned(16))) char lds_stages[];
+__device__ __forceinline__ void walk_balanced(const GemmProblem& a, const GemmProblem& b, char* lds_stages) {
+  constexpr int bn = kWRowsWg / NP;
+  constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
+  const int x = (int)blockIdx.x % kXcds;
+  const int j = (int)blockIdx.x / kXcds;
+  const int J = (int)gridDim.x / kXcds;
+  const Seq q = make_seq<BMA, BMB>(a, b, bn);
+  // the XCD's shared row tiles [b0, b1) and routed tiles [s0, s1)
+  const int rtb = (b.M + BMB - 1) / BMB;
+  const int b0 = rtb * x / kXcds, b1 = rtb * (x + 1) / kXcds;
+  const int nsh = (b1 - b0) * q.ntb;
+  const int s0 = seq_below<BMA>(a, q, (int64_t)q.ca * x / kXcds);
+  const int s1 = seq_below<BMA>(a, q, (int64_t)q.ca * (x + 1) / kXcds);
+  // tile i of the XCD's list: its problem, row tile and column tile
+  auto run = [&](int i) __attribute__((always_inline)) {
+    if (i >= nsh) {
+      i += s0 - nsh;
+      // the last ranked group whose tiles start at or below i
+      const int g = (int)__popcll(__ballot(q.count > 0 && q.tp <= i)) - 1;
+      const int local = i - __builtin_amdgcn_readlane(q.tp, g);
+      const int mt = local / q.nta;
+      const int count = __builtin_amdgcn_readlane(q.count, g);
+      TileRef t;
+      t.n0 = (local - mt * q.nta) * bn;
+      t.pos0 = __builtin_amdgcn_readlane(q.start, g) + mt * BMA;
+      t.rows = min(BMA, count - mt * BMA);
+      t.e = __builtin_amdgcn_readlane(q.e, g);
+      const int nact = (t.rows + 31) >> 5;
+      if constexpr (BMA == 128) {
+        if (nact == 4)
+          lds_tile<BMA, W0, NP, 4>(a, t, lds_stages);
+        else if (nact == 3)
+          lds_tile<BMA, W0, NP, 3>(a, t, lds_stages);
+        else if (nact == 2)
+          lds_tile<BMA, W0, NP, 2>(a, t, lds_stages);
+        else
+          lds_tile<BMA, W0, NP, 1>(a, t, lds_stages);
+      } else {
+        static_assert(BMA == 64, "64- or 128-row tiles");
+        if (nact == 2)
+          lds_tile<BMA, W0, NP, 2>(a, t, lds_stages);
+        else
+          lds_tile<BMA, W0, NP, 1>(a, t, lds_stages);
+      }
+    } else {
+      static_assert(BMB == 64, "64-row shared tiles");
+      const int mt = b0 + i / q.ntb;
+      TileRef t;
+      t.n0 = (i - (mt - b0) * q.ntb) * bn;
+      t.pos0 = mt * BMB;
+      t.rows = min(BMB, b.M - mt * BMB);
+      t.e = 0;
+      if (t.rows > 32)
+        lds_tile<BMB, kBf16KBlocked, NP, 2>(b, t, lds_stages);
+      else
+        lds_tile<BMB, kBf16KBlocked, NP, 1>(b, t, lds_stages);
+    }
+  };
+  // Two rounds at most (small batches): the second round runs in reverse, so
+  // that the workgroups with the list's costliest first tiles take none and
+  // those with its cheapest take the rest.  More rounds walk in order.
+  const int n = nsh + s1 - s0;
+  const bool two = n <= 2 * J;
+  const int rounds = two ? 2 : (n - j + J - 1) / J;
+  for (int k = 0; k < rounds; ++k) {
+    const int it = two && k == 1 ? 2 * J - 1 - j : j + k * J;
+    if (it < n) run(it);
+  }
+}
+
+// The by-class placement's walk of the XCD's list.
+template <WKind W0, int NP>
+__device__ __forceinline__ void walk_classes(const GemmProblem& a, const GemmProblem& b, char* lds_stages) {
   constexpr int bn = kWRowsWg / NP;
   constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
   const int x = (int)blockIdx.x % kXcds;
@@ -1129,26 +1317,55 @@ __global__ void __launch_bounds__(kGThreads, kWgPerCu) k_moe_gemm_lds(GemmProble
   }
 }
 
+template <WKind W0, int NP, bool BAL>
+__global__ void __launch_bounds__(kGThreads, kWgPerCu) k_moe_gemm_lds(GemmProblem a, GemmProblem b) {
+  extern __shared__ __attribute__((aligned(16))) char lds_stages[];
+  if constexpr (BAL)
+    walk_balanced<W0, NP>(a, b, lds_stages);
+  else
+    walk_classes<W0, NP>(a, b, lds_stages);
+}
+
+// Workgroups of the LDS-staged grid: every CU's resident share, a whole
+// number per XCD (the same for both placements).
+template <WKind W0, int NP>
+hipError_t moe_gemm_lds_grid(int* grid) {
+  constexpr size_t lds = kLdsBytes<W0>;
+  static std::atomic<int> cached{0};
+  int g = cached.load(std::memory_order_relaxed);
+  if (g == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    for (const void* f : {(const void*)k_moe_gemm_lds<W0, NP, false>, (const void*)k_moe_gemm_lds<W0, NP, true>})
+      if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_gemm_lds<W0, NP, false>, kGThreads, lds);
+    if (e != hipSuccess) return e;
+    g = (cus / kXcds > 0 ? cus / kXcds : 1) * (per_cu > 0 ? per_cu : 1) * kXcds;
+    cached.store(g, std::memory_order_relaxed);
+  }
+  *grid = g;
+  return hipSuccess;
+}
+
+// The balanced placement once the launch's tiles (bounded from the rows)
+// exceed two rounds of the grid.
 template <WKind W0, int NP>
 hipError_t launch_moe_gemm_lds(const GemmProblem& routed, const GemmProblem& shared, hipStream_t s,
                                const char* name) {
   constexpr size_t lds = kLdsBytes<W0>;
-  static std::atomic<int> cached{0};
-  int grid = cached.load(std::memory_order_relaxed);
-  if (grid == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void*)k_moe_gemm_lds<W0, NP>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds);
-    if (e == hipSuccess)
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_gemm_lds<W0, NP>, kGThreads, lds);
-    if (e != hipSuccess) return e;
-    grid = (cus / kXcds > 0 ? cus / kXcds : 1) * (per_cu > 0 ? per_cu : 1) * kXcds;
-    cached.store(grid, std::memory_order_relaxed);
-  }
-  UOCR_LAUNCH(name, (k_moe_gemm_lds<W0, NP>), dim3(grid), dim3(kGThreads), lds, s, routed, shared);
+  int grid = 0;
+  const hipError_t e = moe_gemm_lds_grid<W0, NP>(&grid);
+  if (e != hipSuccess) return e;
+  constexpr int bn = kWRowsWg / NP;
+  constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
+  const int64_t tiles = (int64_t)((routed.N + bn - 1) / bn) * ((routed.M + BMA - 1) / BMA + routed.max_groups) +
+                        (int64_t)((shared.N + bn - 1) / bn) * ((shared.M + BMB - 1) / BMB);
+  if (tiles > 2 * (int64_t)grid)
+    UOCR_LAUNCH(name, (k_moe_gemm_lds<W0, NP, true>), dim3(grid), dim3(kGThreads), lds, s, routed, shared);
+  else
+    UOCR_LAUNCH(name, (k_moe_gemm_lds<W0, NP, false>), dim3(grid), dim3(kGThreads), lds, s, routed, shared);
   return hipGetLastError();
 }
 
@@ -1181,13 +1398,9 @@ hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared
   if (routed.N % 32 || shared.N % 32 || routed.K % (2 * BK) || shared.K % (2 * BK)) return hipErrorInvalidValue;
   if (routed.kind == kInt8Rows && (routed.K % routed.groups || (routed.K / routed.groups) % BK))
     return hipErrorInvalidValue;
-  const int bn = kWRowsWg / (gu ? 2 : 1);
-  const int64_t units = (int64_t)routed.max_groups * ((routed.N + bn - 1) / bn);
-  const int64_t shared_units = (int64_t)kXcds * ((shared.N + bn - 1) / bn);
-  if ((routed.kind == kInt8Rows && routed.groups > kMaxScaleGroups) || units > kMaxUnits ||
-      shared_units > kMaxUnits) {
+  if ((routed.kind == kInt8Rows && routed.groups > kMaxScaleGroups) || routed.max_groups > kWave) {
     // groups finer than K / 16 (the fragment-load kernel reads each step's scale itself), or more
-    // routed units than the LDS-staged kernel's plan holds
+    // routed groups than the LDS-staged kernel's placement holds (one a lane)
     if (routed.kind == kInt8Rows)
       return gu ? launch_moe_gemm<64, kInt8Rows, 2, false>(routed, shared, s, name)
                 : launch_moe_gemm<64, kInt8Rows, 1, false>(routed, shared, s, name);

@@ -156,7 +156,7 @@ struct GemmProblem {
   Rows rows;
   const int32_t* tile_start;  // [max_groups + 1] m-tile prefix (routed), null for dense
   int max_groups;
-  int M;                      // dense rows (identity)
+  int M;                      // dense rows (identity); routed: the rows of all groups (bounds the tiles)
   // output
   int swiglu;                 // 1: out is bf16 silu(g)*u, row = position; 0: fp32
   uint16_t* outb;

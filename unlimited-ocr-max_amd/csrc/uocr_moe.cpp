@@ -1320,6 +1320,7 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   gu.rows = rows_of(d.g);
   gu.tile_start = d.g.tile_start;
   gu.max_groups = max_groups;
+  gu.M = (int)R;
   gu.swiglu = 1;
   gu.outb = d.hb;
   gu.ldo = F;
