@@ -539,6 +539,68 @@ __device__ __forceinline__ float chain(const Stage<INT8>& st, const float* xp) {
   return acc;
 }
 
+// Two rows' chains over the same weights: each weight converted once, the
+// two fma chains interleaved (each row's chain is chain()'s, in k order from
+// 0: the same bits).  Piece q's activations of both rows are read while the
+// previous piece is computed, as in chain().
+template <bool INT8>
+__device__ __forceinline__ void chain2(const Stage<INT8>& st, const float* xp0, const float* xp1, float& out0,
+                                       float& out1) {
+  constexpr int NP = INT8 ? 8 : 16;
+  constexpr int EP = INT8 ? 16 : 8;
+  constexpr int NV = EP / 4;
+  float a0 = 0.0f, a1 = 0.0f;
+  f32x4 c0[NV], c1[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    c0[v] = *(const f32x4*)(xp0 + 4 * v);
+    c1[v] = *(const f32x4*)(xp1 + 4 * v);
+  }
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    f32x4 n0[NV], n1[NV];
+    if (q + 1 < NP) {
+      int off = (q + 1) * EP;
+      asm volatile("" : "+v"(off) : "v"(a0), "v"(a1));
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        n0[v] = *(const f32x4*)(xp0 + off + 4 * v);
+        n1[v] = *(const f32x4*)(xp1 + off + 4 * v);
+      }
+    }
+    const i32x4 wq = st.v[q];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * v + j;
+        if constexpr (INT8)
+          w[j] = (float)(int8_t)((uint32_t)wq[e >> 2] >> (8 * (e & 3)));
+        else
+          w[j] = (e & 1) ? bf16_hi((uint32_t)wq[e >> 1]) : bf16_lo((uint32_t)wq[e >> 1]);
+      }
+      a0 = __builtin_fmaf(w[0], c0[v].x, a0);
+      a1 = __builtin_fmaf(w[0], c1[v].x, a1);
+      a0 = __builtin_fmaf(w[1], c0[v].y, a0);
+      a1 = __builtin_fmaf(w[1], c1[v].y, a1);
+      a0 = __builtin_fmaf(w[2], c0[v].z, a0);
+      a1 = __builtin_fmaf(w[2], c1[v].z, a1);
+      a0 = __builtin_fmaf(w[3], c0[v].w, a0);
+      a1 = __builtin_fmaf(w[3], c1[v].w, a1);
+    }
+    if (q + 1 < NP) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        c0[v] = n0[v];
+        c1[v] = n1[v];
+      }
+    }
+  }
+  out0 = a0;
+  out1 = a1;
+}
+
 // ----------------------------------------------------------------------------- tasks
 
 struct Ctx {
@@ -616,7 +678,16 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
 __device__ __attribute__((always_inline)) void sgu_rows(const KA FusedArgs& A, const Ctx& C, const Task& k,
                                                         Stage<false>& st) {
   uint64_t* dst = A.p_sgu + C.boff + ((int64_t)(k.a * 2 + k.b) * A.gh + k.c) * A.B * 64 + lane();
-  for (int r = 0; r < A.B; ++r) {
+  // rows two at a time (each weight converted once for both)
+  int r = 0;
+  for (; r + 1 < A.B; r += 2) {
+    launder(st);
+    float v0, v1;
+    chain2<false>(st, C.xs + (r * A.gh + k.c) * kXPad, C.xs + ((r + 1) * A.gh + k.c) * kXPad, v0, v1);
+    st_pair(dst + r * 64, v0, C.tag);
+    st_pair(dst + (r + 1) * 64, v1, C.tag);
+  }
+  if (r < A.B) {
     launder(st);
     st_pair(dst + r * 64, chain<false>(st, C.xs + (r * A.gh + k.c) * kXPad), C.tag);
   }
@@ -697,7 +768,15 @@ __device__ __attribute__((always_inline)) void task_sdn(const KA FusedArgs& A, c
   }
   UOCR_TRACE(A, C.tr, 3);
   uint64_t* dst = A.p_sdn + C.boff + ((int64_t)k.a * A.gfs + g) * A.B * 64 + l;
-  for (int r = 0; r < A.B; ++r) {
+  int r = 0;
+  for (; r + 1 < A.B; r += 2) {
+    launder(st);
+    float v0, v1;
+    chain2<false>(st, C.act + r * 128, C.act + (r + 1) * 128, v0, v1);
+    st_pair(dst + r * 64, v0, C.tag);
+    st_pair(dst + (r + 1) * 64, v1, C.tag);
+  }
+  if (r < A.B) {
     launder(st);
     st_pair(dst + r * 64, chain<false>(st, C.act + r * 128), C.tag);
   }
