@@ -278,7 +278,8 @@ int uocr_moe_decode_rows(float* out, const float* x, int64_t rows, int64_t hidde
  * a GPU shares that GPU's array: calls that overlap in time on one GPU (other
  * streams, other threads) race and must not be made.  A persistent launch whose
  * bounded waits ran out poisons the array's arena (NaN outputs) until
- * uocr_moe_fused_errors on any stream of that device reports and clears it. */
+ * uocr_moe_fused_errors on any stream of that device reports it and clears its
+ * error word; uocr_moe_fused_status reports it in stream order. */
 int uocr_moe_decode_rows_static(float* out, const float* x, int64_t rows, int64_t hidden,
                                 const uocr_moe_layer* layer, int32_t* expert_ids, float* expert_weights,
                                 void* stream, char* err, size_t errlen);
@@ -337,15 +338,18 @@ int uocr_moe_fused_errors(void* stream, uint32_t* errors, char* err, size_t errl
  * kernels/moe_int8.mojo:194-210); the error path of this build's decode kernel. */
 int uocr_moe_fused_status(uint32_t* flag, void* stream, char* err, size_t errlen);
 
-/* Arms a phase trace for the next persistent decode launch: for task i it
- * writes 8 int64 words at buffer[8i] (device memory, `words` long):
- * wall-clock stamps of its phases (0 start, 1 routing known, 2 weights
- * arrived, 3 activations ready, 4 chain done, 5 counter updated, 6 end) and
- * word 7 the wave that ran it.  grid_waves receives the waves of the last
- * launch configuration.  A diagnostic of this build's decode kernel; tracing
- * waits for each task's loads, so a traced launch runs slower.  The trace is
- * compiled in only when the library is built with UOCR_DECODE_TRACE=1; other
- * builds refuse the call. */
+/* Arms a phase trace for the next persistent decode launch (one layer, or a
+ * stack): for task i of layer l it writes 8 int64 words at buffer[8 (i + l R)]
+ * (device memory, `words` long; R = the layout's task capacity + the grid's
+ * workgroups): 100 MHz wall-clock stamps of its phases (0 start, 1 weights
+ * landed, 3 inputs polled, 4 chain done, 2 end, 5 when its wave learnt the
+ * routing), word 6 its kind and word 7 the wave that ran it; each workgroup's
+ * 8 words follow the layer's tasks (its entry, epoch read or x landed, and the
+ * routing's steps).  grid_waves receives the waves of the last traced launch.
+ * A diagnostic of this build's decode kernel; tracing waits for each task's
+ * loads, so a traced launch runs slower.  The trace is compiled in only when
+ * the library is built with UOCR_DECODE_TRACE=1; other builds refuse the
+ * call. */
 int uocr_moe_fused_trace(void* buffer, int64_t words, int* grid_waves, char* err, size_t errlen);
 
 /* ---------------------------------------------------------------------------
