@@ -466,8 +466,7 @@ __device__ __forceinline__ void store_tile(const GemmProblem& P, const TileRef& 
         quad_transpose(v, qd);
         const int col = t.n0 + 32 * w + (m & ~3);
         if (live && col < P.N) {
-          const uint64_t o = (uint64_t)f32_to_bf16_rne(v[0]) | ((uint64_t)f32_to_bf16_rne(v[1]) << 16) |
-                             ((uint64_t)f32_to_bf16_rne(v[2]) << 32) | ((uint64_t)f32_to_bf16_rne(v[3]) << 48);
+          const uint64_t o = (uint64_t)pack_bf16x2(v[0], v[1]) | ((uint64_t)pack_bf16x2(v[2], v[3]) << 32);
           *(UOCR_GLOBAL uint64_t*)(P.outb + orow * P.ldo + col) = o;
         }
       } else {
@@ -706,10 +705,8 @@ __device__ __forceinline__ void lds_step(f32x16 (&acc)[NACT][2], const char* st,
         raw[b][q] = *(const i32x4*)(Bw + (32 * b + m) * RB + 16 * (c ^ (W == kInt8Rows ? swz64(m) : sw)));
       }
     }
-  // Up to two blocks read the A fragments of sub-step k + 1 during sub-step
-  // k; more read each sub-step's own (registers for two waves a SIMD), the
-  // other workgroup on the CU covering the wait.
-  constexpr int AB = MB > 2 ? 1 : 2;
+  // The A fragments of sub-step k + 1 are read during sub-step k.
+  constexpr int AB = 2;
   bf16x8 a[AB][MB];
   auto read_a = [&](bf16x8(&dst)[MB], int sub) {
 #pragma unroll
@@ -743,9 +740,6 @@ __device__ __forceinline__ void lds_step(f32x16 (&acc)[NACT][2], const char* st,
       acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[0], acc[i][0], 0, 0, 0);
       acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[sub % AB][i], bf[1], acc[i][1], 0, 0, 0);
     }
-    // keep each sub-step's dequantisation next to its MFMAs (the two issue in
-    // turn on a SIMD anyway): hoisting it only lengthens register lifetimes
-    if constexpr (MB > 2) __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -758,8 +752,14 @@ __device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t,
   constexpr int NL = St::template loads<NACT>();
   constexpr int RB = St::kBRowBytes;
   constexpr int RPL = 1024 / RB;  // weight rows per load
-  const int tid = (int)threadIdx.x;
-  const int j = lane_id();
+  // The thread index passes through an empty asm per tile, so that what is
+  // derived from it (addresses, swizzles) is computed in the tile and not
+  // hoisted out of the tile loop, where it held about 40 VGPRs across every
+  // K loop (with 256 VGPRs at two waves a SIMD, the 3-4-block loops then read
+  // their A fragments one at a time, each behind its own LDS wait).
+  int tid = (int)threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int j = tid & (kWave - 1);
   const int w = tid >> 6;
   const int m = j & 31, h = j >> 5;
   const int S = P.K / BK;
