@@ -148,11 +148,30 @@ template <WKind W>
 constexpr int kWStages = W == kInt8Rows ? 4 : 2;  // weight steps in flight
 
 struct TileRef {
-  int e;     // expert (routed) or 0
+  int e;     // expert (routed), or the K range of a dense problem in K ranges (else 0)
   int pos0;  // first row position (group order) or first token
   int rows;  // valid rows
   int n0;    // first output column
 };
+
+// K ranges of a problem (a dense K-blocked one may be cut into kparts).
+__host__ __device__ __forceinline__ int parts_of(const GemmProblem& P) {
+  return P.kind == kBf16KBlocked && P.kparts > 1 ? P.kparts : 1;
+}
+
+// K range r of a K-blocked problem ([K / 16][N][16] bf16 weights) as a
+// problem of its own: K / parts, the operands from the range's first k, the
+// sums at outf + r * part_stride.
+__device__ __forceinline__ GemmProblem part_problem(const GemmProblem& P, int r) {
+  GemmProblem Q = P;
+  const int kr = P.K / parts_of(P);
+  Q.K = kr;
+  Q.kparts = 1;
+  Q.a = P.a + (int64_t)r * kr;
+  Q.p[0].w = (const char*)P.p[0].w + (int64_t)r * (kr / 16) * P.N * 32;
+  Q.outf = P.outf + r * P.part_stride;
+  return Q;
+}
 
 // The cut of a problem's column tiles into ranges.
 struct Plan {
@@ -556,10 +575,12 @@ __global__ void __launch_bounds__(kGThreads) k_moe_gemm(GemmProblem a, GemmProbl
   const int na = __builtin_amdgcn_readlane(fa, kWave - 1);
   const int nb = __builtin_amdgcn_readlane(fb, kWave - 1);
   for (int it = j; it < na + nb; it += J) {
-    if (it < na)
+    if (it < na) {
       gemm_tile<BM, W0, NP, VEC>(a, tile_at<BM>(a, pa, x, fa, it, bn), lds);
-    else
-      gemm_tile<BM, kBf16KBlocked, NP, VEC>(b, tile_at<BM>(b, pb, x, fb, it - na, bn), lds);
+    } else {
+      const TileRef t = tile_at<BM>(b, pb, x, fb, it - na, bn);
+      for (int r = 0; r < parts_of(b); ++r) gemm_tile<BM, kBf16KBlocked, NP, VEC>(part_problem(b, r), t, lds);
+    }
   }
 }
 
@@ -762,7 +783,10 @@ __device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t,
   const int j = tid & (kWave - 1);
   const int w = tid >> 6;
   const int m = j & 31, h = j >> 5;
-  const int S = P.K / BK;
+  // the tile's K range: all of K, or range t.e of a problem in K ranges
+  const int parts = parts_of(P);
+  const int S = P.K / BK / parts;
+  const int k0 = parts > 1 ? t.e * S : 0;
 
   // weight rows: load i of the step fills stage rows 64w + RPL i + j / (RB / 16),
   // stored chunk j % (RB / 16) holding chunk (stored) ^ swizzle(row)
@@ -830,7 +854,7 @@ __device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t,
 
   // the loads of step s (clamped to the last step) into stage s % NS
   auto issue = [&](int s) {
-    const int sc = min(s, S - 1);
+    const int sc = k0 + min(s, S - 1);
     char* st = lds + (s % NS) * St::kBytes;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -885,7 +909,13 @@ __device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t,
   }
   // every wave has finished reading the stages (and the scales) before the next tile's loads
   step_barrier<0>();
-  store_tile<32 * NACT, NPROJ>(P, t, acc, w, m, h);
+  if (parts > 1) {
+    GemmProblem Q = P;  // range t.e's sums
+    Q.outf += t.e * P.part_stride;
+    store_tile<32 * NACT, NPROJ>(Q, t, acc, w, m, h);
+  } else {
+    store_tile<32 * NACT, NPROJ>(P, t, acc, w, m, h);
+  }
 }
 
 // Placement for the LDS-staged path, two ways, chosen per launch from the
@@ -931,7 +961,7 @@ __device__ __forceinline__ void lds_tile(const GemmProblem& P, const TileRef& t,
 // per block for bf16, plus 600 a tile for its start and its stores
 // (per-XCD busy times at T = 4096 fit these within about 10 %).
 __device__ __forceinline__ int tile_cost(const GemmProblem& P, int nact) {
-  return (P.K / BK) * (P.kind == kInt8Rows ? 100 + 35 * nact : 65 + 36 * nact) + 600;
+  return (P.K / BK / parts_of(P)) * (P.kind == kInt8Rows ? 100 + 35 * nact : 65 + 36 * nact) + 600;
 }
 
 // One problem's row tiles: rt in all, the last one partial with `apart`
@@ -962,7 +992,7 @@ template <int BMA, int BMB>
 __device__ __forceinline__ Seq make_seq(const GemmProblem& a, const GemmProblem& b, int bn) {
   Seq q;
   q.nta = (a.N + bn - 1) / bn;
-  q.ntb = (b.N + bn - 1) / bn;
+  q.ntb = (b.N + bn - 1) / bn * parts_of(b);  // column tiles of every K range
   const bool routed = a.rows.n_groups != nullptr;
   const int l = lane_id();
   // the group tables for every lane at once, clamped to their size, before
@@ -1228,11 +1258,13 @@ __device__ __forceinline__ void walk_balanced(const GemmProblem& a, const GemmPr
     } else {
       static_assert(BMB == 64, "64-row shared tiles");
       const int mt = b0 + i / q.ntb;
+      const int cr = i - (mt - b0) * q.ntb;  // K range cr / ntr, column tile cr % ntr
+      const int ntr = q.ntb / parts_of(b);
       TileRef t;
-      t.n0 = (i - (mt - b0) * q.ntb) * bn;
+      t.e = cr / ntr;
+      t.n0 = (cr - t.e * ntr) * bn;
       t.pos0 = mt * BMB;
       t.rows = min(BMB, b.M - mt * BMB);
-      t.e = 0;
       if (t.rows > 32)
         lds_tile<BMB, kBf16KBlocked, NP, 2>(b, t, lds_stages);
       else
@@ -1257,7 +1289,8 @@ __device__ __forceinline__ void walk_classes(const GemmProblem& a, const GemmPro
   constexpr int bn = kWRowsWg / NP;
   constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
   const int x = (int)blockIdx.x % kXcds;
-  const int nta = (a.N + bn - 1) / bn, ntb = (b.N + bn - 1) / bn;
+  const int ntr = (b.N + bn - 1) / bn;  // the shared problem's column tiles, in every K range
+  const int nta = (a.N + bn - 1) / bn, ntb = ntr * parts_of(b);
   const int nga = a.rows.n_groups != nullptr ? ldc(a.rows.n_groups) : 1;
   const int j = (int)blockIdx.x / kXcds;
   const int J = (int)gridDim.x / kXcds;
@@ -1299,10 +1332,14 @@ __device__ __forceinline__ void walk_classes(const GemmProblem& a, const GemmPro
       }
     } else {
       static_assert(BMB == 64, "64-row shared tiles");
+      TileRef t = class_tile<BMB>(b, qb, nact, it, bn);
+      const int cr = t.n0 / bn;  // K range cr / ntr, column tile cr % ntr
+      t.e = cr / ntr;
+      t.n0 = (cr - t.e * ntr) * bn;
       if (nact == 2)
-        lds_tile<BMB, kBf16KBlocked, NP, 2>(b, class_tile<BMB>(b, qb, 2, it, bn), lds_stages);
+        lds_tile<BMB, kBf16KBlocked, NP, 2>(b, t, lds_stages);
       else
-        lds_tile<BMB, kBf16KBlocked, NP, 1>(b, class_tile<BMB>(b, qb, 1, it, bn), lds_stages);
+        lds_tile<BMB, kBf16KBlocked, NP, 1>(b, t, lds_stages);
     }
   };
   // Two rounds at most (small batches): the second round runs in reverse, so
@@ -1361,7 +1398,7 @@ hipError_t launch_moe_gemm_lds(const GemmProblem& routed, const GemmProblem& sha
   constexpr int bn = kWRowsWg / NP;
   constexpr int BMA = kLdsBM<W0>, BMB = kLdsBM<kBf16KBlocked>;
   const int64_t tiles = (int64_t)((routed.N + bn - 1) / bn) * ((routed.M + BMA - 1) / BMA + routed.max_groups) +
-                        (int64_t)((shared.N + bn - 1) / bn) * ((shared.M + BMB - 1) / BMB);
+                        (int64_t)((shared.N + bn - 1) / bn) * parts_of(shared) * ((shared.M + BMB - 1) / BMB);
   if (tiles > 2 * (int64_t)grid)
     UOCR_LAUNCH(name, (k_moe_gemm_lds<W0, NP, true>), dim3(grid), dim3(kGThreads), lds, s, routed, shared);
   else
@@ -1392,10 +1429,34 @@ hipError_t launch_quantize(int8_t* q, float* scales, const void* w, int w_bf16, 
 // K granularity of the grouped GEMM: two steps.
 int gemm_bk() { return 2 * BK; }
 
+// Two K ranges for the shared problem where the launch has at most two
+// rounds of tiles (the by-class placement, T = 512: about a tile a
+// workgroup), so that its tiles, twice a routed down tile's K when the shared
+// width is twice the routed one, are not the launch's longest.  With more
+// rounds the extra tiles and the combine's second read cost more (T = 4096:
+// down 123 -> 129 us, the combine 25 -> 29 us).  Both kernels cut the same
+// way; the bound on the tiles is the LDS-staged launch's.
+int gemm_shared_parts(const GemmProblem& routed, const GemmProblem& shared) {
+  if (shared.kind != kBf16KBlocked || shared.swiglu || shared.K % (2 * 2 * BK)) return 1;
+  int grid = 0;
+  const bool int8 = routed.kind == kInt8Rows;
+  const hipError_t e = routed.swiglu ? (int8 ? moe_gemm_lds_grid<kInt8Rows, 2>(&grid) : moe_gemm_lds_grid<kBf16Rows, 2>(&grid))
+                                     : (int8 ? moe_gemm_lds_grid<kInt8Rows, 1>(&grid) : moe_gemm_lds_grid<kBf16Rows, 1>(&grid));
+  if (e != hipSuccess || grid <= 0) return 1;
+  const int bn = kWRowsWg / (routed.swiglu ? 2 : 1);
+  const int BMA = int8 ? kLdsBM<kInt8Rows> : kLdsBM<kBf16Rows>, BMB = kLdsBM<kBf16KBlocked>;
+  const int64_t tiles = (int64_t)((routed.N + bn - 1) / bn) * ((routed.M + BMA - 1) / BMA + routed.max_groups) +
+                        (int64_t)((shared.N + bn - 1) / bn) * 2 * ((shared.M + BMB - 1) / BMB);
+  return tiles <= 2 * (int64_t)grid ? 2 : 1;
+}
+
 hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, hipStream_t s, bool vec) {
   const bool gu = routed.swiglu != 0;
   const char* name = gu ? "gemm_gateup" : "gemm_down";
   if (routed.N % 32 || shared.N % 32 || routed.K % (2 * BK) || shared.K % (2 * BK)) return hipErrorInvalidValue;
+  // K ranges: the shared problem only, each an even number of K steps, fp32 sums
+  if (parts_of(shared) > 1 && (shared.K % (parts_of(shared) * 2 * BK) || shared.swiglu || shared.outf == nullptr))
+    return hipErrorInvalidValue;
   if (routed.kind == kInt8Rows && (routed.K % routed.groups || (routed.K / routed.groups) % BK))
     return hipErrorInvalidValue;
   if ((routed.kind == kInt8Rows && routed.groups > kMaxScaleGroups) || routed.max_groups > kWave) {

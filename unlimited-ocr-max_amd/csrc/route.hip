@@ -746,7 +746,8 @@ template <int W>
 __global__ void __launch_bounds__(kCombineThreads) k_combine(float* __restrict__ out, const float* __restrict__ y,
                                                              int64_t ldy, const float* __restrict__ wts,
                                                              const int32_t* __restrict__ inv,
-                                                             const float* __restrict__ shared, int T, int H, int topk) {
+                                                             const float* __restrict__ shared, int T, int H, int topk,
+                                                             int parts) {
   typedef float vec __attribute__((ext_vector_type(W)));
   const int t = (int)blockIdx.x;
   for (int n = W * (int)threadIdx.x; n < H; n += W * kCombineThreads) {
@@ -771,8 +772,9 @@ __global__ void __launch_bounds__(kCombineThreads) k_combine(float* __restrict__
         }
       }
     }
-    if (shared) {
-      const vec sh = *(const UOCR_GLOBAL vec*)(shared + (int64_t)t * H + n);
+    // the shared experts' sums, one K range after another (T x H floats apart)
+    for (int r = 0; shared && r < parts; ++r) {
+      const vec sh = *(const UOCR_GLOBAL vec*)(shared + ((int64_t)r * T + t) * H + n);
 #pragma unroll
       for (int c = 0; c < W; ++c) acc[c] = acc[c] + sh[c];
     }
@@ -871,15 +873,16 @@ hipError_t launch_route_small(const float* logits, int T, int E, int topk, int r
 }
 
 hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* wts, const int32_t* inv,
-                          const float* shared, int T, int H, int topk, hipStream_t s) {
+                          const float* shared, int T, int H, int topk, hipStream_t s, int shared_parts) {
   if (T <= 0) return hipSuccess;
+  if (shared_parts < 1) return hipErrorInvalidValue;
   const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (H % 4 == 0 && ldy % 4 == 0 && a16(out) && a16(y) && (shared == nullptr || a16(shared)))
     UOCR_LAUNCH("combine", k_combine<4>, dim3(T), dim3(kCombineThreads), 0, s, out, y, ldy, wts, inv, shared, T, H,
-                topk);
+                topk, shared_parts);
   else
     UOCR_LAUNCH("combine", k_combine<1>, dim3(T), dim3(kCombineThreads), 0, s, out, y, ldy, wts, inv, shared, T, H,
-                topk);
+                topk, shared_parts);
   return hipGetLastError();
 }
 

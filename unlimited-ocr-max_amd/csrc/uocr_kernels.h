@@ -127,10 +127,11 @@ hipError_t launch_logits_topk_group(float* logits, uint16_t* xb, const float* x,
 hipError_t launch_route_small(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32,
                               float* wts, const GroupTables& g, hipStream_t s);
 
-// out[t, n] = fma-chain over j of wts[t*k+j] * y[row(t*k+j), n] from 0, + shared[t, n].
+// out[t, n] = fma-chain over j of wts[t*k+j] * y[row(t*k+j), n] from 0, then
+// + shared[r][t, n] for r < shared_parts in turn (parts T x H floats apart).
 // row(i) = inv ? inv[i] : i.  shared may be null.
 hipError_t launch_combine(float* out, const float* y, int64_t ldy, const float* wts, const int32_t* inv,
-                          const float* shared, int T, int H, int topk, hipStream_t s);
+                          const float* shared, int T, int H, int topk, hipStream_t s, int shared_parts = 1);
 
 // ---- int8 dequantisation and the prefill grouped GEMM (gemm.hip) ----
 
@@ -163,6 +164,12 @@ struct GemmProblem {
   float* outf;
   int64_t ldo;
   int out_by_position;        // 1: output row = position in group order, 0: row id
+  // A dense K-blocked problem (the shared one) in kparts > 1 K ranges of
+  // K / kparts: each range's sums are computed from zero and stored at
+  // outf + r * part_stride, the caller adds them (both kernels cut K the
+  // same way, so they give the same bits)
+  int kparts;
+  int64_t part_stride;
 };
 // bm: rows per tile, 64 or 128.  vec: every weight pointer is 16-byte
 // aligned; else the weights are read at any alignment (bm must be 64), with
@@ -170,6 +177,8 @@ struct GemmProblem {
 // group, itself a multiple of 64); a routed problem has at most 64 groups.
 hipError_t launch_gemm_pair(const GemmProblem& routed, const GemmProblem& shared, int bm, hipStream_t s,
                             bool vec = true);
+// The K ranges to cut the shared problem into for this pair (1 or 2).
+int gemm_shared_parts(const GemmProblem& routed, const GemmProblem& shared);
 
 // ---- the n-gram logit guard (ngram.hip) ----
 

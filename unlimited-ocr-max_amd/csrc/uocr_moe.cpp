@@ -931,7 +931,7 @@ static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
   d.hb = c.take<uint16_t>(R * L->ffn);
   d.hsb = c.take<uint16_t>(T * L->shared_ffn);
   d.y = c.take<float>(R * L->hidden);
-  d.sh = c.take<float>(T * L->hidden);
+  d.sh = c.take<float>(2 * T * L->hidden);  // the shared experts' down sums, in up to two K ranges
   d.total = c.take<int32_t>(L->num_experts);
   d.base = c.take<int32_t>((int64_t)route_count_blocks((int)T) * L->num_experts);
   d.hist = c.take<int32_t>((int64_t)fused_route_blocks((int)T) * L->num_experts);
@@ -1371,8 +1371,14 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
   sdn.outb = nullptr;
   sdn.outf = d.sh;
   sdn.ldo = H;
+  // The shared down projection in two K ranges of Fs / 2 at small T, each its own tiles (summed by the
+  // combine): its K steps a tile are twice a routed down tile's, which made the shared tiles the
+  // launch's longest at T = 512 (down 43 -> 35 us).
+  sdn.kparts = gemm_shared_parts(dn, sdn);
+  sdn.part_stride = T * H;
   e = launch_gemm_pair(dn, sdn, BM, s, vec);
-  if (e == hipSuccess) e = launch_combine(out, d.y, H, d.wts, d.g.inv, d.sh, (int)T, H, (int)L->top_k, s);
+  if (e == hipSuccess)
+    e = launch_combine(out, d.y, H, d.wts, d.g.inv, d.sh, (int)T, H, (int)L->top_k, s, sdn.kparts);
   if (e == hipSuccess && expert_ids) e = hipMemcpyAsync(expert_ids, d.ids, R * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
   if (e == hipSuccess && expert_weights)
     e = hipMemcpyAsync(expert_weights, d.wts, R * sizeof(float), hipMemcpyDeviceToDevice, s);
