@@ -1123,6 +1123,10 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     // a router task's weights do not depend on x: they load while x is staged
     // (defined for every wave, so that no value is carried from the previous layer)
     float w[kMaxJ];
+    // The launch's epoch word (first layer): loaded before x so that its round
+    // trip overlaps x's; after x it added a round trip to every routing.
+    uint32_t epoch_word = 0u;
+    if (layer == 0 && threadIdx.x == kCtlThread) epoch_word = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
     if constexpr (STACK) {
 #pragma unroll
       for (int j = 0; j < kMaxJ; ++j) w[j] = 0.0f;
@@ -1197,14 +1201,15 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
     }
     // One load of the epoch per workgroup and launch (3 072 waves loading the
     // one word at once would queue every workgroup's start behind it), shared
-    // through LDS.  The last wave does it (and the arrival count below): its
+    // through LDS.  The last wave loads it (before x, above) and makes the
+    // arrival count below: its
     // first work is to wait for the logits, while the router tasks run on the
     // first waves.
     if (threadIdx.x == kCtlThread) {
       *r_done = 0;
       *C.landed = 0;
       if (layer == 0) {
-        *lds_epoch = ld_word(A.ctl + C_EPOCH + (blockIdx.x % kSpread) * kLine);
+        *lds_epoch = epoch_word;
         if (kTrace && A.trace != nullptr) {
           asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
           A.trace[twg + blockIdx.x * 8 + 7] = (int64_t)wall_clock64();

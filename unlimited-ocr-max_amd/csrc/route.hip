@@ -26,6 +26,7 @@ namespace {
 // tokens' x rows rounded to bf16 (xb), when asked: the prefill GEMM's A
 // operand.
 constexpr int kLogitsMaxH = 2048;
+constexpr int kXcds = kFusedXcds;  // XCDs; workgroup b runs on XCD b % kXcds
 
 // The first workgroup of a launch clears `n` words for a later kernel of the
 // same stream (the routing's counters).
@@ -165,6 +166,121 @@ __device__ __forceinline__ void logits_tile(float* __restrict__ logits, uint16_t
     const int e = 4 * j % EW + e_row;
     if ((l & 15) == 0 && t0 + t < T && e0 + e < E) logits[(int64_t)(t0 + t) * E + e0 + e] = sums[j];
   }
+}
+
+// logits_tile for H = 64 NJ (NJ compile-time): the same chains and trees,
+// the operands in a ring of D register slots, so that the loads of step
+// j + D are issued as step j's fmas are done and D steps are in flight at
+// once (logits_tile waits for each batch of JB steps before its fmas).
+// Slot t holds token t0 + (t + rot) % TW (every slot's chains are its own, so
+// the order of the slots changes no bits); the xb rows of slots 0 .. XK-1 are
+// written.
+template <int TW, int EW, int NJ, int XK>
+__device__ __forceinline__ void logits_ring(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                            const float* __restrict__ x, int64_t ldx,
+                                            const float* __restrict__ router, int T, int E, int t0, int e0,
+                                            int rot) {
+  constexpr int D = 2;
+  constexpr int H = NJ * kWave;
+  if (t0 >= T || e0 >= E) return;
+  const int l = lane_id();
+  // wave-uniform row bases (rows past the end repeat the last one), the lane's
+  // element k = l + 64 j at byte 4 l + 256 j of a row
+  const UOCR_GLOBAL char* xr[TW];
+  const UOCR_GLOBAL char* wr[EW];
+  uint16_t* br[TW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    const int64_t row = min(t0 + (t + rot) % TW, T - 1);
+    xr[t] = (const UOCR_GLOBAL char*)(x + row * ldx);
+    br[t] = xb + row * H;
+  }
+#pragma unroll
+  for (int e = 0; e < EW; ++e) wr[e] = (const UOCR_GLOBAL char*)(router + (int64_t)min(e0 + e, E - 1) * H);
+  // (the instruction's offset field holds below 4 KiB: 16 steps from each of
+  // these lane offsets, kept opaque so that none is folded back into it)
+  uint32_t lo[(NJ + 15) / 16];
+#pragma unroll
+  for (int i = 0; i < (NJ + 15) / 16; ++i) {
+    lo[i] = 4u * (uint32_t)l + 4096u * i;
+    asm volatile("" : "+v"(lo[i]));
+  }
+  float p[TW][EW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t)
+#pragma unroll
+    for (int e = 0; e < EW; ++e) p[t][e] = 0.0f;
+  float xa[D][TW], wa[D][EW];
+#pragma unroll
+  for (int s = 0; s < D; ++s) {
+#pragma unroll
+    for (int t = 0; t < TW; ++t) xa[s][t] = *(const UOCR_GLOBAL float*)(xr[t] + (lo[0] + 256u * s));
+#pragma unroll
+    for (int e = 0; e < EW; ++e) wa[s][e] = *(const UOCR_GLOBAL float*)(wr[e] + (lo[0] + 256u * s));
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int s = j % D;
+    // (a row past the end stores the last row's value again, to its place)
+#pragma unroll
+    for (int t = 0; t < XK; ++t) br[t][l + j * kWave] = f32_to_bf16_rne(xa[s][t]);
+#pragma unroll
+    for (int t = 0; t < TW; ++t)
+#pragma unroll
+      for (int e = 0; e < EW; ++e) p[t][e] = __builtin_fmaf(xa[s][t], wa[s][e], p[t][e]);
+    if (j + D < NJ) {
+      const uint32_t o = lo[(j + D) / 16] + 256u * ((j + D) % 16);
+#pragma unroll
+      for (int t = 0; t < TW; ++t) xa[s][t] = *(const UOCR_GLOBAL float*)(xr[t] + o);
+#pragma unroll
+      for (int e = 0; e < EW; ++e) wa[s][e] = *(const UOCR_GLOBAL float*)(wr[e] + o);
+    }
+    // each step's loads stay after its fmas (hoisted higher, they would hold
+    // more slots than the ring's)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  static_assert(EW % 4 == 0, "a quad of values shares its token");
+  float flat[TW * EW], sums[TW * EW / 4];
+#pragma unroll
+  for (int t = 0; t < TW; ++t)
+#pragma unroll
+    for (int e = 0; e < EW; ++e) flat[t * EW + e] = p[t][e];
+  tree_sum_quads(flat, sums);
+  const int e_row = tree_row_value(l >> 4);
+#pragma unroll
+  for (int j = 0; j < TW * EW / 4; ++j) {
+    const int t = t0 + (4 * j / EW + rot) % TW;
+    const int e = 4 * j % EW + e_row;
+    if ((l & 15) == 0 && t < T && e0 + e < E) logits[(int64_t)t * E + e0 + e] = sums[j];
+  }
+}
+
+template <int TW, int EW, int NJ>
+__global__ void __launch_bounds__(256) k_logits_ring(float* __restrict__ logits, uint16_t* __restrict__ xb,
+                                                     const float* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ router, int T, int E,
+                                                     int32_t* __restrict__ zero, int nzero) {
+  zero_words_once(zero, nzero);
+  // Workgroup b runs on XCD b % 8: the E / EW expert blocks of one block of
+  // 4 TW tokens run on the same XCD, whose L2 then fetches those x rows once.
+  const int b = (int)blockIdx.x;
+  const int neb = (E + EW - 1) / EW;
+  const int slot = b / kXcds;
+  const int tb = (slot / neb) * kXcds + b % kXcds;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int t0 = (tb * 4 + w) * TW;
+  const int eb = slot % neb;
+  const int e0 = eb * EW;
+  // The xb rows: each of the 4 expert blocks (E = 4 EW, which the launch
+  // checks) writes 2 of a wave's 8 tokens, its slots 0 and 1 (tokens 2 eb and
+  // 2 eb + 1), so that no block's waves take longer than the others'.  (One
+  // copy of the loop with the stores and one without: a branch in each step
+  // would split it into blocks that the scheduler cannot order.)
+  static_assert(TW == 8, "2 of 8 tokens per expert block");
+  if (xb != nullptr)
+    logits_ring<TW, EW, NJ, 2>(logits, xb, x, ldx, router, T, E, t0, e0, 2 * eb);
+  else
+    logits_ring<TW, EW, NJ, 0>(logits, xb, x, ldx, router, T, E, t0, e0, 0);
 }
 
 template <int TW, int EW>
@@ -556,10 +672,30 @@ __global__ void __launch_bounds__(kRouteWaves * 64) k_logits_topk(
   const int t0 = b * kFusedTokens;
   const int nt = min(kFusedTokens, T - t0);
   const int nj = H / kWave;
-  const int e0 = 4 * w;
+  // wave w's 4 experts, rotated by the workgroup (the workgroups of an XCD then
+  // ask for different router rows at the same moment, not all for the same
+  // rows in the same order)
+  const int e0 = 4 * ((w + b) % kRouteWaves);
   const bool active = e0 < E;
   if (tid < 64) cnt[tid] = 0;
-  // the first batch of router values, issued before the x rows are staged
+  // The x rows' loads are issued first, then every router value: the x rows
+  // land first, and once they are in LDS the fmas of step j wait only for
+  // step j's router values (with the router loads first, staging x waited for
+  // all of them).
+  const bool xvec = (((uintptr_t)x | (uintptr_t)(ldx * 4) | (uintptr_t)(H * 4)) & 15) == 0;
+  constexpr int kXv = kFusedTokens * kLogitsMaxH / 4 / (kRouteWaves * kWave);
+  const int h4 = H / 4;
+  f32x4 xv[kXv];
+  if (xvec) {
+    // 16-byte pieces, every thread's loads issued before the first is stored
+    // (a loop of single loads waited out one memory latency per element)
+#pragma unroll
+    for (int j = 0; j < kXv; ++j) {
+      const int i = tid + j * kRouteWaves * kWave;
+      const int t = min(i / h4, nt - 1);
+      xv[j] = *(const UOCR_GLOBAL f32x4*)(x + (int64_t)(t0 + t) * ldx + 4 * (i - (i / h4) * h4));
+    }
+  }
   const float* wl = router + (int64_t)min(e0, E - 1) * H + l;
   int64_t wo[4];
 #pragma unroll
@@ -571,18 +707,7 @@ __global__ void __launch_bounds__(kRouteWaves * 64) k_logits_topk(
 #pragma unroll
       for (int e = 0; e < 4; ++e) wa[jj][e] = ldg(wl + wo[e] + min(jj, nj - 1) * kWave);
   }
-  if ((((uintptr_t)x | (uintptr_t)(ldx * 4) | (uintptr_t)(H * 4)) & 15) == 0) {
-    // 16-byte pieces, every thread's loads issued before the first is stored
-    // (a loop of single loads waited out one memory latency per element)
-    constexpr int kXv = kFusedTokens * kLogitsMaxH / 4 / (kRouteWaves * kWave);
-    const int h4 = H / 4;
-    f32x4 xv[kXv];
-#pragma unroll
-    for (int j = 0; j < kXv; ++j) {
-      const int i = tid + j * kRouteWaves * kWave;
-      const int t = min(i / h4, nt - 1);
-      xv[j] = *(const f32x4*)(x + (int64_t)(t0 + t) * ldx + 4 * (i - (i / h4) * h4));
-    }
+  if (xvec) {
 #pragma unroll
     for (int j = 0; j < kXv; ++j) {
       const int i = tid + j * kRouteWaves * kWave;
@@ -787,6 +912,14 @@ __global__ void __launch_bounds__(kCombineThreads) k_combine(float* __restrict__
 hipError_t launch_logits(float* logits, const float* x, int64_t ldx, const float* router, int T, int E, int H,
                          uint16_t* xb, hipStream_t s, int32_t* zero, int nzero) {
   if (T <= 0) return hipSuccess;
+  if (H == 20 * kWave && E == 64 && T >= 2048) {
+    // every XCD an equal share of the token blocks (those past T return at once)
+    const int ntb = (T + 31) / 32;
+    const dim3 grid((unsigned)(kXcds * ((ntb + kXcds - 1) / kXcds) * ((E + 15) / 16)));
+    UOCR_LAUNCH("logits", (k_logits_ring<8, 16, 20>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, zero,
+                nzero);
+    return hipGetLastError();
+  }
   if (H % kWave == 0 && T >= 2048) {
     const dim3 grid((unsigned)((E + 15) / 16), (unsigned)((T + 31) / 32));
     UOCR_LAUNCH("logits", (k_logits_tile<8, 16>), grid, dim3(256), 0, s, logits, xb, x, ldx, router, T, E, H, zero, nzero);
