@@ -633,6 +633,7 @@ __device__ __attribute__((always_inline)) void router_load(const KA FusedArgs& A
 }
 
 // Logits of expert e for tokens t0 .. t1-1.
+template <bool STACK>
 __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A, const Ctx& C, int e, int t0, int t1,
                                                            const float (&w)[kMaxJ]) {
   const int l = lane();
@@ -640,12 +641,23 @@ __device__ __attribute__((always_inline)) void router_task(const KA FusedArgs& A
   uint64_t* dst = A.logits + C.boff + (blockIdx.x % kXcds) * kLogitCopyWords + e;
   if (t1 - t0 == 1) {
     const float* xr = C.xs + t0 * A.gh * kXPad + l;
-    // (issuing every read before the chain made the layer slower at one
-    // token, though the chain itself got shorter)
+    // In the stack (router weights loaded during the previous layer, so the
+    // chain starts as x lands) the 20 x reads of H = 1280 go out before the
+    // chain, without the loop bound's branch between them (179.2 -> 176.5 us
+    // for 11 layers at one token); in one layer, whose chain waits for the
+    // router rows' first load anyway, the same made the launch slower.
     float p = 0.0f;
+    if (STACK && nk == 20) {
+      float xv[20];
 #pragma unroll
-    for (int j = 0; j < kMaxJ; ++j)
-      if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
+      for (int j = 0; j < 20; ++j) xv[j] = xr[(j >> 1) * kXPad + kWave * (j & 1)];
+#pragma unroll
+      for (int j = 0; j < 20; ++j) p = __builtin_fmaf(xv[j], w[j], p);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kMaxJ; ++j)
+        if (j < nk) p = __builtin_fmaf(xr[(j >> 1) * kXPad + kWave * (j & 1)], w[j], p);
+    }
     const float v = tree_sum(p);
     if (l == 0) st_pair_xcd(dst + t0 * 64, v, C.tag);
   } else {
@@ -1233,7 +1245,7 @@ __global__ void __launch_bounds__(kThreads) k_decode_fused(FusedArgs args) {
       C.tr = kTrace ? r_e + layer * (int)A.trace_layer : r_e;
       if (traced) UOCR_TRACE(A, C.tr, 0);
       if (traced) UOCR_TRACE_LOADS(A, C.tr);
-      router_task(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
+      router_task<STACK>(A, C, r_e, r_t0, min(A.B, r_t0 + A.r_tok), w);
       if (traced) UOCR_TRACE(A, C.tr, 2);
       if (traced && kTrace && A.trace != nullptr && lane() == 0) A.trace[(int64_t)C.tr * 8 + 7] = rank;
     }
