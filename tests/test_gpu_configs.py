@@ -80,6 +80,15 @@ def test_prefill_t4096_zipf(oracle, full_int8) -> None:
     assert hist.max() > 1000
 
 
+def test_prefill_t2049_partial_token_block(oracle, full_int8) -> None:
+    """T = 2049 (Zipf): the T >= 2048 router logits kernel's last token block holds one token, its
+    padding slots repeat that row, and its expert blocks each write their share of the bf16 x rows
+    (a missing or misplaced row would change those tokens' outputs beyond the bar)."""
+    x, layer = _zipf_layer(oracle, full_int8, 2049, 2049)
+    hist = _prefill_check(oracle, layer, x, "prefill int8 T=2049 Zipf")
+    assert hist.sum() == 2049 * 6
+
+
 def test_prefill_t4096_adversarial(oracle, full_int8) -> None:
     """All 4096 tokens on experts 0-5 (bias +10 through the constant feature): six 4096-row groups."""
     x, layer = _zipf_layer(oracle, full_int8, 4096, 4097)

@@ -46,7 +46,7 @@ def full_bf16(oracle):
 # ----------------------------------------------------------------------------- gate
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 300, 4096])
+@pytest.mark.parametrize("T", [1, 8, 64, 300, 2049, 2111, 4096])
 def test_gate_bitwise(oracle, T) -> None:
     from uocr_moe import gate
 
