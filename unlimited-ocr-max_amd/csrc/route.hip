@@ -540,24 +540,18 @@ __global__ void __launch_bounds__(1024) k_group(const int32_t* __restrict__ ids,
 // ---------------------------------------------------------------- prefill routing over many workgroups
 //
 // k_topk_count: a wave per token (softmax + top-k), 16 tokens per workgroup;
-// the workgroup counts its rows per expert and reserves that many places of
-// each expert with one atomic add on the expert's row total (cleared by the
-// logits launch), keeping the returned offset.  k_group_scatter: from the
-// totals, every workgroup derives the groups and row tiles (workgroup 0
-// writes those tables) and places the rows of kScatterSpan counting
-// workgroups at their reserved offsets.  Within one counting workgroup's
-// rows of an expert, and between counting workgroups, the order is the
-// atomics' (each row is computed on its own, so nothing depends on it).
+// the workgroup's rows per expert go to hist[b] (every expert, zeros
+// included), and k_group_scatter_hist places them as for the fused routing
+// (16-token blocks).  A reservation by one atomic add per (workgroup, expert)
+// on the experts' row totals took about half the launch at T=4096 (256
+// workgroups on 64 addresses) and made the order inside a group the atomics'.
 
 constexpr int kCountThreads = 1024;
 constexpr int kCountTokens = kCountThreads / 64;
-constexpr int kScatterThreads = 256;
-constexpr int kScatterSpan = 1;  // counting workgroups per scatter workgroup
 
 __global__ void __launch_bounds__(kCountThreads) k_topk_count(const float* __restrict__ logits, int T, int E, int topk,
                                                               int renorm, int32_t* __restrict__ ids32,
-                                                              float* __restrict__ wts, int32_t* __restrict__ total,
-                                                              int32_t* __restrict__ base) {
+                                                              float* __restrict__ wts, int32_t* __restrict__ hist) {
   __shared__ int cnt[kRouteMaxExperts];
   __shared__ uint64_t scratch[kCountTokens][kTopkScratch];
   const int b = (int)blockIdx.x;
@@ -574,68 +568,7 @@ __global__ void __launch_bounds__(kCountThreads) k_topk_count(const float* __res
   for (int64_t r = (int64_t)t0 * topk + tid; r < (int64_t)t1 * topk; r += kCountThreads)
     atomicAdd(&cnt[clamp_expert(ids32[r], E)], 1);
   __syncthreads();
-  for (int e = tid; e < E; e += kCountThreads) {
-    const int c = cnt[e];
-    if (c > 0) stg(base + (int64_t)b * E + e, atomicAdd(total + e, c));
-  }
-}
-
-__global__ void __launch_bounds__(kScatterThreads) k_group_scatter(const int32_t* __restrict__ ids, int T, int E,
-                                                                   int topk, int bm, const int32_t* __restrict__ total,
-                                                                   const int32_t* __restrict__ base, GroupTables g) {
-  __shared__ int cursor[kRouteMaxExperts];
-  __shared__ int start_of[kRouteMaxExperts];
-  __shared__ int part[12];
-  const int tid = (int)threadIdx.x;
-  const int w = tid / kWave;
-  const int tot = tid < E ? ldg(total + tid) : 0;
-  const int tiles = tot > 0 ? (tot + bm - 1) / bm : 0;
-  const int nz = tot > 0 ? 1 : 0;
-  const int ic = wave_scan_i(tot), it = wave_scan_i(tiles), in = wave_scan_i(nz);
-  if (lane_id() == kWave - 1) {
-    part[w] = ic;
-    part[4 + w] = it;
-    part[8 + w] = in;
-  }
-  __syncthreads();
-  int pc = 0, pt = 0, pn = 0;
-  for (int v = 0; v < w; ++v) {
-    pc += part[v];
-    pt += part[4 + v];
-    pn += part[8 + v];
-  }
-  const int start = pc + ic - tot, tile0 = pt + it - tiles, grp = pn + in - nz;
-  if (tid < E) {
-    start_of[tid] = start;
-    if (blockIdx.x == 0) {
-      if (tot > 0) {
-        stg(g.group_expert + grp, tid);
-        stg(g.group_start + grp, start);
-        if (g.tile_start) stg(g.tile_start + grp, tile0);
-      }
-      if (tid == E - 1) {
-        stg(g.group_start + grp + nz, start + tot);
-        if (g.tile_start) stg(g.tile_start + grp + nz, tile0 + tiles);
-        stg(g.n_groups, grp + nz);
-      }
-    }
-  }
-  const int nblocks = (T + kCountTokens - 1) / kCountTokens;
-  const int b0 = (int)blockIdx.x * kScatterSpan;
-  const int b1 = min(nblocks, b0 + kScatterSpan);
-  for (int b = b0; b < b1; ++b) {
-    __syncthreads();  // start_of is written; the previous block's cursors are done
-    // (offsets of experts with no row in block b are stale and never read)
-    if (tid < E) cursor[tid] = start_of[tid] + ldg(base + (int64_t)b * E + tid);
-    __syncthreads();
-    const int64_t r0 = (int64_t)b * kCountTokens * topk;
-    const int64_t r1 = min((int64_t)T * topk, r0 + (int64_t)kCountTokens * topk);
-    for (int64_t r = r0 + tid; r < r1; r += kScatterThreads) {
-      const int pos = atomicAdd(&cursor[clamp_expert(ldg(ids + r), E)], 1);
-      stg(g.group_rows + pos, (int32_t)r);
-      if (g.inv) stg(g.inv + r, pos);
-    }
-  }
+  for (int e = tid; e < E; e += kCountThreads) stg(hist + (int64_t)b * E + e, cnt[e]);
 }
 
 // ---------------------------------------------------------------- prefill routing, T below 2048
@@ -786,24 +719,35 @@ __global__ void __launch_bounds__(kRouteWaves * 64) k_logits_topk(
   if (tid < E) stg(hist + (int64_t)b * E + tid, cnt[tid]);
 }
 
+constexpr int kScatterRows = 256;  // rows ranked at once (a pass per 256 rows of a block)
+
 __global__ void __launch_bounds__(256) k_group_scatter_hist(const int32_t* __restrict__ ids, int T, int E, int topk,
-                                                            int bm, int blocks, const int32_t* __restrict__ hist,
-                                                            GroupTables g) {
+                                                            int bm, int blocks, int block_tokens,
+                                                            const int32_t* __restrict__ hist, GroupTables g) {
   __shared__ int part_before[4][64];
+  __shared__ int bids[kScatterRows];
   __shared__ int part_tot[4][64];
   __shared__ int cursor[64];
   const int b = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int e = tid & 63;
   const int c = tid >> 6;
-  // four threads per expert, each over every fourth counting workgroup
+  // four threads per expert, each over every fourth counting workgroup, 16
+  // loads in flight at a time (indices past the last block re-read it and
+  // are not counted)
+  constexpr int kBatch = 16;
   int before = 0, tot = 0;
   if (e < E) {
-#pragma unroll 4
-    for (int v = c; v < blocks; v += 4) {
-      const int h = ldg(hist + (int64_t)v * E + e);
-      before += v < b ? h : 0;
-      tot += h;
+    for (int v0 = c; v0 < blocks; v0 += 4 * kBatch) {
+      int h[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) h[i] = ldg(hist + (int64_t)min(v0 + 4 * i, blocks - 1) * E + e);
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int v = v0 + 4 * i;
+        before += v < b ? h[i] : 0;
+        tot += v < blocks ? h[i] : 0;
+      }
     }
   }
   part_before[c][e] = before;
@@ -833,13 +777,30 @@ __global__ void __launch_bounds__(256) k_group_scatter_hist(const int32_t* __res
       }
     }
   }
-  __syncthreads();
-  const int64_t r0 = (int64_t)b * kFusedTokens * topk;
-  const int64_t r1 = min((int64_t)T * topk, r0 + (int64_t)kFusedTokens * topk);
-  for (int64_t r = r0 + tid; r < r1; r += 256) {
-    const int pos = atomicAdd(&cursor[clamp_expert(ldg(ids + r), E)], 1);
-    stg(g.group_rows + pos, (int32_t)r);
-    if (g.inv) stg(g.inv + r, pos);
+  // The block's rows in row order within each group: row r goes after the
+  // rows of the same expert before it in the block (a rank, not an atomic, so
+  // the order does not depend on the schedule), 256 rows a pass.
+  const int64_t r0 = (int64_t)b * block_tokens * topk;
+  const int nr = (int)min((int64_t)T * topk - r0, (int64_t)block_tokens * topk);
+  for (int c0 = 0; c0 < nr; c0 += kScatterRows) {
+    const int n = min(kScatterRows, nr - c0);
+    __syncthreads();  // the cursors are final for the rows before this pass
+    if (tid < n) bids[tid] = clamp_expert(ldg(ids + r0 + c0 + tid), E);
+    __syncthreads();
+    if (tid < n) {
+      const int e = bids[tid];
+      int rank = 0;
+      for (int i = 0; i < tid; ++i) rank += bids[i] == e ? 1 : 0;
+      const int pos = cursor[e] + rank;
+      stg(g.group_rows + pos, (int32_t)(r0 + c0 + tid));
+      if (g.inv) stg(g.inv + r0 + c0 + tid, pos);
+    }
+    __syncthreads();  // every rank read the cursors
+    if (tid < E) {
+      int c = 0;
+      for (int i = 0; i < n; ++i) c += bids[i] == tid ? 1 : 0;
+      cursor[tid] += c;
+    }
   }
 }
 
@@ -971,14 +932,14 @@ hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTab
 int route_count_blocks(int T) { return (T + kCountTokens - 1) / kCountTokens; }
 
 hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
-                             int bm, const GroupTables& g, int32_t* total, int32_t* base, hipStream_t s) {
+                             int bm, const GroupTables& g, int32_t* hist, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  if (E > kRouteMaxExperts || E > kScatterThreads) return hipErrorInvalidValue;
+  if (E > kRouteMaxExperts) return hipErrorInvalidValue;
   const int blocks = route_count_blocks(T);
   UOCR_LAUNCH("topk_count", k_topk_count, dim3(blocks), dim3(kCountThreads), 0, s, logits, T, E, topk, renorm, ids32,
-              wts, total, base);
-  UOCR_LAUNCH("group_scatter", k_group_scatter, dim3((blocks + kScatterSpan - 1) / kScatterSpan),
-              dim3(kScatterThreads), 0, s, ids32, T, E, topk, bm, total, base, g);
+              wts, hist);
+  UOCR_LAUNCH("group_scatter", k_group_scatter_hist, dim3(blocks), dim3(256), 0, s, ids32, T, E, topk, bm, blocks,
+              kCountTokens, hist, g);
   return hipGetLastError();
 }
 
@@ -993,7 +954,7 @@ hipError_t launch_logits_topk_group(float* logits, uint16_t* xb, const float* x,
   UOCR_LAUNCH("logits_topk", k_logits_topk, dim3(blocks), dim3(kRouteWaves * kWave), 0, s, logits, xb, x, ldx,
               router, T, E, H, topk, renorm, ids32, wts, hist);
   UOCR_LAUNCH("group_scatter", k_group_scatter_hist, dim3(blocks), dim3(256), 0, s, ids32, T, E, topk, bm, blocks,
-              hist, g);
+              kFusedTokens, hist, g);
   return hipGetLastError();
 }
 

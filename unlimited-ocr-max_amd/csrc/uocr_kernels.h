@@ -108,13 +108,12 @@ struct GroupTables {
 // Groups R rows by their clamped expert id (ascending expert).
 hipError_t launch_group(const int32_t* ids, int R, int E, int bm, const GroupTables& g, hipStream_t s);
 // Prefill routing over many workgroups (E <= 64): softmax + top-k of T
-// tokens, then the grouping of their T*topk rows.  `total` (E ints) must be
-// zero when the first kernel starts (launch_logits clears it); `base` holds
-// route_count_blocks(T) * E ints of scratch.
+// tokens and their rows per expert in 16-token blocks, then the grouping of
+// their T*topk rows.  `hist` holds route_count_blocks(T) * E ints of scratch.
 constexpr int kRouteMaxExperts = 64;  // a lane per expert in the top-k
 int route_count_blocks(int T);
 hipError_t launch_topk_group(const float* logits, int T, int E, int topk, int renorm, int32_t* ids32, float* wts,
-                             int bm, const GroupTables& g, int32_t* total, int32_t* base, hipStream_t s);
+                             int bm, const GroupTables& g, int32_t* hist, hipStream_t s);
 // Prefill routing for T < 2048 (E <= 64): logits, softmax + top-k and
 // per-workgroup counts in one launch (xb as launch_logits), then the
 // grouping.  hist holds fused_route_blocks(T) * E ints of scratch.

@@ -915,9 +915,7 @@ struct PrefillBufs {
   uint16_t* hsb;
   float* y;
   float* sh;
-  int32_t* total;  // rows per expert (routing counters)
-  int32_t* base;   // per counting workgroup: its first place per expert
-  int32_t* hist;   // per counting workgroup: its rows per expert (T < 2048)
+  int32_t* hist;   // per counting workgroup: its rows per expert
 };
 
 static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
@@ -932,8 +930,7 @@ static PrefillBufs carve_prefill(Carve& c, const uocr_moe_layer* L, int64_t T) {
   d.hsb = c.take<uint16_t>(T * L->shared_ffn);
   d.y = c.take<float>(R * L->hidden);
   d.sh = c.take<float>(2 * T * L->hidden);  // the shared experts' down sums, in up to two K ranges
-  d.total = c.take<int32_t>(L->num_experts);
-  d.base = c.take<int32_t>((int64_t)route_count_blocks((int)T) * L->num_experts);
+  // (the T < 2048 routing's 4-token blocks outnumber the T >= 2048 one's 16-token blocks)
   d.hist = c.take<int32_t>((int64_t)fused_route_blocks((int)T) * L->num_experts);
   return d;
 }
@@ -1298,10 +1295,9 @@ int uocr_moe_forward(float* out, const float* x, int64_t seq, int64_t hidden, co
     e = launch_logits_topk_group(d.logits, d.xb, x, H, L->router, (int)T, E, H, (int)L->top_k, L->renormalize, d.ids,
                                  d.wts, BM, d.g, d.hist, s);
   } else {
-    e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s, d.total, E);
+    e = launch_logits(d.logits, x, H, L->router, (int)T, E, H, d.xb, s);
     if (e == hipSuccess)
-      e = launch_topk_group(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, d.wts, BM, d.g, d.total, d.base,
-                            s);
+      e = launch_topk_group(d.logits, (int)T, E, (int)L->top_k, L->renormalize, d.ids, d.wts, BM, d.g, d.hist, s);
   }
   if (e != hipSuccess) return hip_fail(err, errlen, op, e);
   const int max_groups = (int)(E < R ? E : R);
