@@ -247,6 +247,26 @@ def test_prefill_small_shapes(oracle, int8, group, H, F, T) -> None:
     assert rel <= 1e-2
 
 
+@pytest.mark.parametrize(("T", "topk"), [(2048, 6), (2100, 20)])
+def test_prefill_many_tokens_small_layer(oracle, T, topk) -> None:
+    """T >= 2048 routes through the top-k counting launch (16 tokens a block) and the shared scatter;
+    top-k 20 gives 320 rows a block, which the scatter ranks in two passes of 256 (a narrow layer, so the
+    logits take the general tile kernel)."""
+    layer = oracle.make_layer(70 + topk, E=64, H=256, F=256, n_shared=1, topk=topk, int8=True, std=0.05,
+                              router_std=0.1)
+    moe = moe_for(layer)
+    x = oracle.rmsnorm_rows(np.random.default_rng(900 + T), T, 256)
+    out, ids, wts = moe(t(x), routing=True)
+    ids_o, wts_o = oracle.moe_gate(x, layer.router, topk)
+    assert np.array_equal(n(ids), ids_o)
+    assert bits_equal(n(wts), wts_o)
+    got = n(out)
+    ref = oracle.moe_layer_f64(x, layer, ids_o, wts_o, bf16_dequant=True)
+    rel = oracle.rel_err(got, ref)
+    print(f"[uocr] prefill small E=64 H=256 T={T} top-k {topk}: rel {rel:.3e}")
+    assert rel <= 1e-2
+
+
 def test_prefill_128_row_tiles(oracle, full_int8) -> None:
     """T = 2048 (12288 routed rows): the launch runs 128-row tiles."""
     moe = moe_for(full_int8)
