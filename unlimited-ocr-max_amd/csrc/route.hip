@@ -725,7 +725,7 @@ __global__ void __launch_bounds__(256) k_group_scatter_hist(const int32_t* __res
                                                             int bm, int blocks, int block_tokens,
                                                             const int32_t* __restrict__ hist, GroupTables g) {
   __shared__ int part_before[4][64];
-  __shared__ int bids[kScatterRows];
+  __shared__ int wcnt[4][64];  // a pass's rows per (wave, expert)
   __shared__ int part_tot[4][64];
   __shared__ int cursor[64];
   const int b = (int)blockIdx.x;
@@ -779,28 +779,31 @@ __global__ void __launch_bounds__(256) k_group_scatter_hist(const int32_t* __res
   }
   // The block's rows in row order within each group: row r goes after the
   // rows of the same expert before it in the block (a rank, not an atomic, so
-  // the order does not depend on the schedule), 256 rows a pass.
+  // the order does not depend on the schedule), 256 rows a pass: the rank
+  // inside the wave from ballots over the expert id's bits, plus the rows of
+  // that expert in the pass's earlier waves.
   const int64_t r0 = (int64_t)b * block_tokens * topk;
   const int nr = (int)min((int64_t)T * topk - r0, (int64_t)block_tokens * topk);
+  const int w = tid >> 6;
   for (int c0 = 0; c0 < nr; c0 += kScatterRows) {
-    const int n = min(kScatterRows, nr - c0);
+    const bool live = tid < nr - c0;
     __syncthreads();  // the cursors are final for the rows before this pass
-    if (tid < n) bids[tid] = clamp_expert(ldg(ids + r0 + c0 + tid), E);
+    wcnt[w][tid & 63] = 0;
+    // (lanes past the rows take key 64, which no row has)
+    const int ex = live ? clamp_expert(ldg(ids + r0 + c0 + tid), E) : 64;
+    const uint64_t same = same_key_lanes(ex, 7);
+    const int below = lanes_below(same);
     __syncthreads();
-    if (tid < n) {
-      const int e = bids[tid];
-      int rank = 0;
-      for (int i = 0; i < tid; ++i) rank += bids[i] == e ? 1 : 0;
-      const int pos = cursor[e] + rank;
+    if (live && below == 0) wcnt[w][ex] = __builtin_popcountll(same);
+    __syncthreads();
+    if (live) {
+      int pos = cursor[ex] + below;
+      for (int v = 0; v < w; ++v) pos += wcnt[v][ex];
       stg(g.group_rows + pos, (int32_t)(r0 + c0 + tid));
       if (g.inv) stg(g.inv + r0 + c0 + tid, pos);
     }
-    __syncthreads();  // every rank read the cursors
-    if (tid < E) {
-      int c = 0;
-      for (int i = 0; i < n; ++i) c += bids[i] == tid ? 1 : 0;
-      cursor[tid] += c;
-    }
+    __syncthreads();  // every position read the cursors
+    if (tid < E) cursor[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
   }
 }
 
